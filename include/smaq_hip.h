@@ -1,0 +1,210 @@
+/*
+ * smaq_hip.h -- C ABI of libsmaq_hip.so, the MI355X (gfx950) kernels behind the
+ * SMAQ quantized-KV hot path.
+ *
+ * Conventions
+ *  - Every entry point is extern "C", takes plain device pointers, element
+ *    counts and strides, and an opaque hipStream_t (void*), and returns an int
+ *    status: SMAQ_OK (0) or a negative code.  smaq_last_error() returns a
+ *    thread-local message for the last failure on the calling thread.
+ *  - The caller allocates every output and workspace (torch does, on the
+ *    Python side).  Entry points never allocate, never synchronise the stream,
+ *    and keep no mutable global state (re-entrant).
+ *  - dtype codes: SMAQ_F32 = 0, SMAQ_F16 = 1, SMAQ_BF16 = 2.
+ *  - "rows" inputs are addressed as row r = o * n_inner + i at element offset
+ *    o * s_outer + i * s_inner with a contiguous last dim; outputs are dense
+ *    row-major in r order.  This covers the [1, Hkv, T, D] transpose views the
+ *    reference's store passes to its codecs (smaq/store.py:86-87).
+ *
+ * Each declaration names the reference interface (file:line under
+ * gauravsaini/smaq) whose arithmetic it replaces.
+ */
+#ifndef SMAQ_HIP_H_
+#define SMAQ_HIP_H_
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { SMAQ_F32 = 0, SMAQ_F16 = 1, SMAQ_BF16 = 2 };
+enum { SMAQ_OK = 0, SMAQ_EINVAL = -1, SMAQ_EUNSUPPORTED = -2, SMAQ_ELAUNCH = -3 };
+
+/* Library version (major * 10000 + minor * 100 + patch). */
+int smaq_version(void);
+/* Message for the last non-zero status returned on this thread. */
+const char* smaq_last_error(void);
+
+/*
+ * Value bit-packer.  Replaces quantize_values (smaq/kv_cache.py:50-91):
+ * per group of `group` elements, scale = max((max-min)/(2^bits-1), 1e-10),
+ * zero = min, code = clamp(round_half_even((v-zero)/scale), 0, 2^bits-1),
+ * every op rounded to the value dtype.  2-bit codes pack 4 per byte, 4-bit 2
+ * per byte (low bits first), other widths 1 per byte.
+ *   data_out   [rows, D/vpb] uint8     scales_out, zeros_out [rows, D/group] vdtype
+ */
+int smaq_pack_values(const void* v, int vdtype, long long n_outer, long long n_inner,
+                     long long s_outer, long long s_inner, int D, int bits, int group,
+                     void* data_out, void* scales_out, void* zeros_out, void* stream);
+
+/*
+ * Value dequantiser.  Replaces unpack_values + dequantize_values
+ * (smaq/kv_cache.py:29-47,94-103): out = float(code) * scale + zero (fp32).
+ */
+int smaq_dequant_values(const void* data, const void* scales, const void* zeros, int sdtype,
+                        long long rows, int D, int bits, int group, float* out, void* stream);
+
+/*
+ * Scalar key encoder.  Replaces SMAQQuantizer.quantize (smaq/quantizer.py:138-145)
+ * and RotationAdapter.quantize (smaq/weighted_scalar.py:347-355):
+ * n = ||k|| (key dtype), u = k / (n + 1e-10) (key dtype), y = u @ M^T (fp32),
+ * optionally y *= coord_scales, code = #{bounds[i] < y}, packed
+ * max(1, 8/bits) codes per byte.  Mt is M transposed, [D][D] fp32 row-major.
+ *   codes_out [rows, ceil(D/vpb)] uint8    norms_out [rows] kdtype
+ *   tie_count (nullable): += number of y within 1e-6 (relative) of a bound.
+ */
+int smaq_encode_scalar(const void* k, int kdtype, long long n_outer, long long n_inner,
+                       long long s_outer, long long s_inner, int D, const float* Mt,
+                       const float* coord_scales, const float* bounds, int n_bounds, int bits,
+                       void* codes_out, void* norms_out, unsigned long long* tie_count,
+                       void* stream);
+
+/*
+ * Row transform y = (x @ M^T) [* coord_scales] in fp32 with a sequential FMA
+ * chain over D.  Replaces SMAQQuantizer.rotate_query (smaq/quantizer.py:131-136)
+ * and RotationAdapter.rotate_query (smaq/weighted_scalar.py:342-345).
+ */
+int smaq_rotate_rows(const void* x, int xdtype, long long rows, int D, const float* Mt,
+                     const float* coord_scales, float* out, void* stream);
+
+/*
+ * Scalar key dequantiser.  Replaces SMAQQuantizer.dequantize
+ * (smaq/quantizer.py:147-152; inv_scales = NULL, Mt = E_inv^T) and
+ * RotationAdapter.dequantize (smaq/weighted_scalar.py:357-363; Mt = R):
+ * k_hat = ((c[code] [* inv_scales]) @ Mt) * norm, written as odtype.
+ */
+int smaq_dequant_scalar(const void* codes, const void* norms, int ndtype, long long rows, int D,
+                        int bits, const float* centroids, const float* inv_scales, const float* Mt,
+                        void* out, int odtype, void* stream);
+
+/*
+ * Scores against scalar-coded keys.  Replaces the score path of
+ * SMAQQuantizer.attention_score / smaq_attention_scores
+ * (smaq/quantizer.py:154-184, smaq/triton_kernels.py:102-114,190-208):
+ * out[b, r, t] = ((qrot[b, r] . c[code[b, t]]) * norm[b, t]) [* scale].
+ *   qrot [batch, nq, D] fp32; codes [batch, N, P] uint8; norms [batch, N];
+ *   out [batch, nq, N] in odtype.  has_scale = 0 skips the scale multiply.
+ */
+int smaq_scores_scalar(const float* qrot, long long batch, long long nq, long long N, int D,
+                       const void* codes, int bits, const void* norms, int ndtype,
+                       const float* centroids, int has_scale, float scale, void* out, int odtype,
+                       void* stream);
+
+/*
+ * Block-VQ key encoder.  Replaces SMAQBlockVQ.quantize (smaq/block_vq.py:216-244):
+ * per block b, x = k_b @ E_b^T, d = sqrt(clamp_min(-2 x.c + |x|^2 + |c|^2, 0))
+ * (torch.cdist's matmul form), index = first argmin.
+ *   E_blocks [nb][bd][bd]; centroids [nb][nc][bd] fp32; idx_out [rows, nb] uint8.
+ *   tie_count (nullable): += number of (row, block) whose two best distances
+ *   are within 1e-6 (relative).
+ */
+int smaq_encode_blockvq(const void* k, int kdtype, long long n_outer, long long n_inner,
+                        long long s_outer, long long s_inner, int n_blocks, int block_dim,
+                        int n_centroids, const float* E_blocks, const float* centroids,
+                        void* idx_out, unsigned long long* tie_count, void* stream);
+
+/*
+ * Block-VQ dequantiser.  Replaces SMAQBlockVQ.dequantize (smaq/block_vq.py:246-267):
+ * k_hat[r, b*bd + i] = decoded[b][idx[r, b]][i] (fp32).
+ */
+int smaq_dequant_blockvq(const void* idx, long long rows, int n_blocks, int block_dim,
+                         int n_centroids, const float* decoded, float* out, void* stream);
+
+/*
+ * Fused quantized-KV attention (decode and prefill).  Replaces
+ * compute_hybrid_attention (smaq/score.py:23-72) with its per-head score loop
+ * (smaq/score.py:75-96), value dequantisation (smaq/kv_cache.py:94-103) and
+ * weighted sums (smaq/score.py:113-124): one softmax over [history; recent]
+ * logits, each part cast to the output dtype before the sum.
+ *
+ * History token t of sequence b, KV head h, lives at row
+ *   contiguous: h * hist_head_stride + hist_seq_start[b] + t
+ *   paged:      (block_table[b * max_blocks + t / block_size] * Hkv + h) * block_size
+ *               + t % block_size
+ * and every per-token array (key bytes, norms, value bytes, scales, zeros) is
+ * indexed by that row.  Rows of queries: (b, t, hq) with hq -> KV head hq / g.
+ */
+enum { SMAQ_KEY_SCALAR = 0, SMAQ_KEY_BLOCKVQ = 1 };
+
+typedef struct smaq_attn_params {
+  /* shapes */
+  int batch;        /* sequences */
+  int q_len;        /* query tokens per sequence (T) */
+  int n_q_heads;    /* Hq */
+  int n_kv_heads;   /* Hkv */
+  int head_dim;     /* D */
+  float scale;      /* softmax scale (1/sqrt(D) when the caller passes None) */
+  /* queries, fp32 [batch][q_len][Hq][D]: q_hist is the query as the history
+     codec scores it (rotated for scalar codes), q_exact the plain query. */
+  const float* q_hist;
+  const float* q_exact;
+  /* causal extension: NULL = no mask (reference semantics); else int64
+     [batch][q_len] absolute positions; key j is visible iff pos_j <= q_pos. */
+  const long long* q_positions;
+  /* history (compressed) segment */
+  int has_history;
+  int key_format;          /* SMAQ_KEY_SCALAR or SMAQ_KEY_BLOCKVQ */
+  const void* key_bytes;   /* [rows][key_row_bytes] uint8 */
+  int key_row_bytes;
+  int key_bits;            /* scalar: bits per code */
+  const void* key_norms;   /* scalar: [rows], norm_dtype */
+  int norm_dtype;
+  const float* key_lut;    /* scalar: centroids [2^bits]; block-VQ: decoded [nb][nc][bd] */
+  int vq_blocks, vq_block_dim, vq_centroids;
+  const void* val_bytes;   /* [rows][val_row_bytes] uint8 */
+  int val_row_bytes;
+  int val_bits, val_group;
+  const void* val_scales;  /* [rows][D/group], val_dtype */
+  const void* val_zeros;
+  int val_dtype;
+  const long long* hist_len;        /* [batch] history tokens per sequence; NULL: all
+                                       sequences hold max_hist_len tokens */
+  const long long* hist_seq_start;  /* contiguous layout: [batch] start row; NULL:
+                                       sequence b starts at row b * max_hist_len */
+  long long hist_head_stride;       /* contiguous layout: rows between heads */
+  const int* block_table;           /* paged layout, NULL for contiguous */
+  int max_blocks;
+  int block_size;
+  long long hist_pos_offset;        /* absolute position of history token 0 */
+  /* recent (exact) segment: [batch][recent_stride_t][Hkv][D] in recent_dtype */
+  int has_recent;
+  const void* recent_k;
+  const void* recent_v;
+  int recent_dtype;
+  const long long* recent_len;      /* [batch]; NULL: all hold max_recent_len */
+  long long recent_batch_stride;    /* elements between sequences */
+  long long recent_pos_offset;      /* absolute position of recent token 0 */
+  /* output [batch][q_len][Hq][D] in out_dtype */
+  void* out;
+  int out_dtype;
+  /* workspace from smaq_attn_workspace_bytes */
+  void* workspace;
+  long long workspace_bytes;
+  /* max history length over the batch (sizes the split grid) */
+  long long max_hist_len;
+  long long max_recent_len;
+  /* 0 = run everything; else a bit mask of phases to launch, so a caller can
+     time them apart: 1 = history partials, 2 = recent partials, 4 = combine.
+     Phases communicate through the workspace, launched in order on one
+     stream. */
+  int phases;
+} smaq_attn_params;
+
+/* Bytes of workspace smaq_attn_hybrid needs for these parameters. */
+long long smaq_attn_workspace_bytes(const smaq_attn_params* p);
+int smaq_attn_hybrid(const smaq_attn_params* p, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SMAQ_HIP_H_ */

@@ -1,0 +1,353 @@
+"""ctypes binding of libsmaq_hip.so (the C ABI declared in include/smaq_hip.h).
+
+This is the only module that talks to the native library.  Every op here
+validates its tensors, allocates outputs with torch on the tensors' device,
+launches on torch's current stream and maps a non-zero status to an
+exception: ``ValueError`` for invalid arguments (the reference's own error
+type for bad shapes), ``RuntimeError`` for anything else.  There is no second
+code path: if the library is missing, or a tensor is not on a GPU, the call
+raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch  # imported before the library so one HIP runtime is shared
+
+_LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libsmaq_hip.so"
+_lib = None
+
+F32, F16, BF16 = 0, 1, 2
+_DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
+KEY_SCALAR, KEY_BLOCKVQ = 0, 1
+
+c_void_p, c_int, c_ll, c_float = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_float
+c_ull_p = ctypes.POINTER(ctypes.c_ulonglong)
+
+
+class AttnParams(ctypes.Structure):
+    """Mirror of ``smaq_attn_params`` (include/smaq_hip.h)."""
+
+    _fields_ = [
+        ("batch", c_int), ("q_len", c_int), ("n_q_heads", c_int), ("n_kv_heads", c_int),
+        ("head_dim", c_int), ("scale", c_float),
+        ("q_hist", c_void_p), ("q_exact", c_void_p), ("q_positions", c_void_p),
+        ("has_history", c_int), ("key_format", c_int), ("key_bytes", c_void_p),
+        ("key_row_bytes", c_int), ("key_bits", c_int), ("key_norms", c_void_p),
+        ("norm_dtype", c_int), ("key_lut", c_void_p),
+        ("vq_blocks", c_int), ("vq_block_dim", c_int), ("vq_centroids", c_int),
+        ("val_bytes", c_void_p), ("val_row_bytes", c_int), ("val_bits", c_int),
+        ("val_group", c_int), ("val_scales", c_void_p), ("val_zeros", c_void_p),
+        ("val_dtype", c_int),
+        ("hist_len", c_void_p), ("hist_seq_start", c_void_p), ("hist_head_stride", c_ll),
+        ("block_table", c_void_p), ("max_blocks", c_int), ("block_size", c_int),
+        ("hist_pos_offset", c_ll),
+        ("has_recent", c_int), ("recent_k", c_void_p), ("recent_v", c_void_p),
+        ("recent_dtype", c_int), ("recent_len", c_void_p), ("recent_batch_stride", c_ll),
+        ("recent_pos_offset", c_ll),
+        ("out", c_void_p), ("out_dtype", c_int),
+        ("workspace", c_void_p), ("workspace_bytes", c_ll),
+        ("max_hist_len", c_ll), ("max_recent_len", c_ll),
+        ("phases", c_int),
+    ]
+
+
+_SIGS = {
+    "smaq_version": (c_int, []),
+    "smaq_last_error": (ctypes.c_char_p, []),
+    "smaq_pack_values": (c_int, [c_void_p, c_int, c_ll, c_ll, c_ll, c_ll, c_int, c_int, c_int,
+                                 c_void_p, c_void_p, c_void_p, c_void_p]),
+    "smaq_dequant_values": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_ll, c_int, c_int,
+                                    c_int, c_void_p, c_void_p]),
+    "smaq_encode_scalar": (c_int, [c_void_p, c_int, c_ll, c_ll, c_ll, c_ll, c_int, c_void_p,
+                                   c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p,
+                                   c_void_p, c_void_p]),
+    "smaq_rotate_rows": (c_int, [c_void_p, c_int, c_ll, c_int, c_void_p, c_void_p, c_void_p,
+                                 c_void_p]),
+    "smaq_dequant_scalar": (c_int, [c_void_p, c_void_p, c_int, c_ll, c_int, c_int, c_void_p,
+                                    c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
+    "smaq_scores_scalar": (c_int, [c_void_p, c_ll, c_ll, c_ll, c_int, c_void_p, c_int, c_void_p,
+                                   c_int, c_void_p, c_int, c_float, c_void_p, c_int, c_void_p]),
+    "smaq_encode_blockvq": (c_int, [c_void_p, c_int, c_ll, c_ll, c_ll, c_ll, c_int, c_int, c_int,
+                                    c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "smaq_dequant_blockvq": (c_int, [c_void_p, c_ll, c_int, c_int, c_int, c_void_p, c_void_p,
+                                     c_void_p]),
+    "smaq_attn_workspace_bytes": (c_ll, [ctypes.POINTER(AttnParams)]),
+    "smaq_attn_hybrid": (c_int, [ctypes.POINTER(AttnParams), c_void_p]),
+}
+
+EXPORTED = tuple(_SIGS)
+
+
+def library_path() -> Path:
+    return _LIB_PATH
+
+
+def lib():
+    """Loads libsmaq_hip.so once; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not _LIB_PATH.exists():
+            raise RuntimeError(
+                f"smaq_amd native library missing at {_LIB_PATH}; build it with "
+                "`python -m smaq_amd.csrc.build` (hipcc --offload-arch=gfx950)")
+        handle = ctypes.CDLL(str(_LIB_PATH), mode=os.RTLD_NOW | os.RTLD_LOCAL)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def _check(status: int, what: str) -> None:
+    if status == 0:
+        return
+    msg = lib().smaq_last_error().decode(errors="replace")
+    if status == -1:
+        raise ValueError(msg or f"{what}: invalid argument")
+    raise RuntimeError(f"{what} failed ({status}): {msg}")
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODE[dt]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {dt}; expected float32, float16 or bfloat16") from None
+
+
+def require_gpu(*tensors) -> torch.device:
+    """All tensors must live on one GPU: the kernels have no CPU path."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError(
+                "smaq_amd runs its codecs and attention as HIP kernels; got a tensor on "
+                f"{t.device}. Move inputs to the GPU (cuda device).")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} vs {t.device}")
+    return dev
+
+
+def row_view(x: torch.Tensor):
+    """Express x[..., D] (last dim contiguous) as rows r = o * n_inner + i at
+    offset o * s_outer + i * s_inner.  Returns None if no such 2-level form
+    exists (the caller then makes the tensor contiguous)."""
+    if x.dim() == 0 or x.stride(-1) != 1:
+        return None
+    lead = [(s, st) for s, st in zip(x.shape[:-1], x.stride()[:-1]) if s != 1]
+    if not lead:
+        return 1, 1, 0, 0
+    # merge dims that are already contiguous with each other
+    merged = [list(lead[0])]
+    for s, st in lead[1:]:
+        ps, pst = merged[-1]
+        if pst == s * st:
+            merged[-1] = [ps * s, st]
+        else:
+            merged.append([s, st])
+    if len(merged) == 1:
+        (n, st), = merged
+        return 1, n, 0, st
+    if len(merged) == 2:
+        (no, so), (ni, si) = merged
+        return no, ni, so, si
+    return None
+
+
+def _rows_args(x: torch.Tensor):
+    rv = row_view(x)
+    if rv is None:
+        x = x.contiguous()
+        rv = row_view(x)
+    return x, rv
+
+
+# ---------------------------------------------------------------- values ---
+
+def _value_row_bytes(D: int, bits: int) -> int:
+    return D // (4 if bits == 2 else (2 if bits == 4 else 1))
+
+
+def pack_values(v: torch.Tensor, bits: int, group_size: int):
+    """quantize_values on the GPU -> (data u8 [..., D/vpb], scales, zeros [..., D/G])."""
+    dev = require_gpu(v)
+    D = v.shape[-1]
+    if D % group_size != 0:
+        raise ValueError(f"head_dim {D} must be divisible by group_size {group_size}")
+    lead = v.shape[:-1]
+    vpb = 4 if bits == 2 else (2 if bits == 4 else 1)
+    if D % vpb != 0:
+        raise ValueError(f"head_dim {D} must be divisible by {vpb} for {bits}-bit packing")
+    v, (no, ni, so, si) = _rows_args(v)
+    data = torch.empty(*lead, D // vpb, dtype=torch.uint8, device=dev)
+    scales = torch.empty(*lead, D // group_size, dtype=v.dtype, device=dev)
+    zeros = torch.empty_like(scales)
+    _check(lib().smaq_pack_values(_ptr(v), dtype_code(v.dtype), no, ni, so, si, D, bits, group_size,
+                                  _ptr(data), _ptr(scales), _ptr(zeros), _stream(dev)),
+           "smaq_pack_values")
+    return data, scales, zeros
+
+
+def dequant_values(data, scales, zeros, bits: int, group_size: int) -> torch.Tensor:
+    dev = require_gpu(data, scales, zeros)
+    data, scales, zeros = data.contiguous(), scales.contiguous(), zeros.contiguous()
+    vpb = 4 if bits == 2 else (2 if bits == 4 else 1)
+    D = data.shape[-1] * vpb
+    rows = data.numel() // max(1, data.shape[-1])
+    out = torch.empty(*data.shape[:-1], D, dtype=torch.float32, device=dev)
+    _check(lib().smaq_dequant_values(_ptr(data), _ptr(scales), _ptr(zeros), dtype_code(scales.dtype),
+                                     rows, D, bits, group_size, _ptr(out), _stream(dev)),
+           "smaq_dequant_values")
+    return out
+
+
+# ---------------------------------------------------------------- scalar ---
+
+class TieCounter:
+    """Device-side counter the encoders add boundary/argmin ties into."""
+
+    def __init__(self, device):
+        self.t = torch.zeros(1, dtype=torch.int64, device=device)
+
+    def ptr(self):
+        return ctypes.c_void_p(self.t.data_ptr())
+
+    def value(self) -> int:
+        return int(self.t.item())
+
+
+def encode_scalar(k: torch.Tensor, Mt: torch.Tensor, bounds: torch.Tensor, bits: int,
+                  coord_scales: torch.Tensor | None = None, ties: TieCounter | None = None):
+    """Scalar key encoder -> (packed codes u8 [..., ceil(D/vpb)], norms [...] in k.dtype)."""
+    dev = require_gpu(k, Mt, bounds, coord_scales)
+    D = k.shape[-1]
+    lead = k.shape[:-1]
+    vpb = max(1, 8 // bits)
+    k, (no, ni, so, si) = _rows_args(k)
+    codes = torch.empty(*lead, (D + vpb - 1) // vpb, dtype=torch.uint8, device=dev)
+    norms = torch.empty(lead, dtype=k.dtype, device=dev)
+    Mt = Mt.to(torch.float32).contiguous()
+    bounds = bounds.to(torch.float32).contiguous()
+    cs = None if coord_scales is None else coord_scales.to(torch.float32).contiguous()
+    _check(lib().smaq_encode_scalar(_ptr(k), dtype_code(k.dtype), no, ni, so, si, D, _ptr(Mt), _ptr(cs),
+                                    _ptr(bounds), bounds.numel(), bits, _ptr(codes), _ptr(norms),
+                                    ties.ptr() if ties else None, _stream(dev)),
+           "smaq_encode_scalar")
+    return codes, norms
+
+
+def rotate_rows(x: torch.Tensor, Mt: torch.Tensor, coord_scales: torch.Tensor | None = None):
+    """(x @ M^T) [* coord_scales] in fp32, Mt = M^T contiguous."""
+    dev = require_gpu(x, Mt, coord_scales)
+    D = x.shape[-1]
+    xc = x.contiguous()
+    mt = Mt.to(torch.float32).contiguous()
+    out = torch.empty(*x.shape[:-1], Mt.shape[1], dtype=torch.float32, device=dev)
+    cs = None if coord_scales is None else coord_scales.to(torch.float32).contiguous()
+    _check(lib().smaq_rotate_rows(_ptr(xc), dtype_code(xc.dtype), xc.numel() // max(D, 1), D, _ptr(mt),
+                                  _ptr(cs), _ptr(out), _stream(dev)), "smaq_rotate_rows")
+    return out
+
+
+def rotate_rows_into(x: torch.Tensor, Mt: torch.Tensor, coord_scales, out: torch.Tensor) -> None:
+    """In-place variant of rotate_rows: x contiguous, out fp32 of x's shape."""
+    D = x.shape[-1]
+    _check(lib().smaq_rotate_rows(_ptr(x), dtype_code(x.dtype), x.numel() // max(D, 1), D, _ptr(Mt),
+                                  _ptr(coord_scales), _ptr(out), _stream(x.device)), "smaq_rotate_rows")
+
+
+def dequant_scalar(codes, norms, bits: int, D: int, centroids, Mt, inv_scales=None,
+                   out_dtype=torch.float32):
+    dev = require_gpu(codes, norms, centroids, Mt, inv_scales)
+    codes, norms = codes.contiguous(), norms.contiguous()
+    cents = centroids.to(torch.float32).contiguous()
+    mt = Mt.to(torch.float32).contiguous()
+    rows = norms.numel()
+    out = torch.empty(*norms.shape, D, dtype=out_dtype, device=dev)
+    inv = None if inv_scales is None else inv_scales.to(torch.float32).contiguous()
+    _check(lib().smaq_dequant_scalar(_ptr(codes), _ptr(norms), dtype_code(norms.dtype), rows, D, bits,
+                                     _ptr(cents), _ptr(inv), _ptr(mt), _ptr(out), dtype_code(out_dtype),
+                                     _stream(dev)), "smaq_dequant_scalar")
+    return out
+
+
+def scores_scalar(qrot: torch.Tensor, codes: torch.Tensor, norms: torch.Tensor, bits: int,
+                  centroids: torch.Tensor, scale, out_dtype):
+    """qrot [B, nq, D] fp32, codes [B, N, P], norms [B, N] -> [B, nq, N]."""
+    dev = require_gpu(qrot, codes, norms, centroids)
+    B, nq, D = qrot.shape
+    N = codes.shape[1]
+    # bind every converted copy to a name: its storage must outlive the launch
+    q, c, n = qrot.contiguous(), codes.contiguous(), norms.contiguous()
+    cents = centroids.to(torch.float32).contiguous()
+    out = torch.empty(B, nq, N, dtype=out_dtype, device=dev)
+    _check(lib().smaq_scores_scalar(_ptr(q), B, nq, N, D, _ptr(c), bits, _ptr(n), dtype_code(n.dtype),
+                                    _ptr(cents), 0 if scale is None else 1,
+                                    0.0 if scale is None else float(scale), _ptr(out), dtype_code(out_dtype),
+                                    _stream(dev)), "smaq_scores_scalar")
+    return out
+
+
+# -------------------------------------------------------------- block VQ ---
+
+def encode_blockvq(k: torch.Tensor, E_blocks: torch.Tensor, centroids: torch.Tensor,
+                   ties: TieCounter | None = None) -> torch.Tensor:
+    dev = require_gpu(k, E_blocks, centroids)
+    nb, nc, bd = centroids.shape
+    if k.shape[-1] != nb * bd:
+        raise ValueError(f"key dim {k.shape[-1]} != n_blocks * block_dim = {nb * bd}")
+    lead = k.shape[:-1]
+    k, (no, ni, so, si) = _rows_args(k)
+    eb = E_blocks.to(torch.float32).contiguous()
+    cents = centroids.to(torch.float32).contiguous()
+    idx = torch.empty(*lead, nb, dtype=torch.uint8, device=dev)
+    _check(lib().smaq_encode_blockvq(_ptr(k), dtype_code(k.dtype), no, ni, so, si, nb, bd, nc, _ptr(eb),
+                                     _ptr(cents), _ptr(idx), ties.ptr() if ties else None, _stream(dev)),
+           "smaq_encode_blockvq")
+    return idx
+
+
+def dequant_blockvq(idx: torch.Tensor, decoded: torch.Tensor) -> torch.Tensor:
+    dev = require_gpu(idx, decoded)
+    nb, nc, bd = decoded.shape
+    if idx.dtype != torch.uint8:
+        if int(idx.max()) > 255 or int(idx.min()) < 0:
+            raise ValueError("block-VQ indices must be in [0, 255]")
+        idx = idx.to(torch.uint8)
+    idx = idx.contiguous()
+    dec = decoded.to(torch.float32).contiguous()
+    rows = idx.numel() // nb
+    out = torch.empty(*idx.shape[:-1], nb * bd, dtype=torch.float32, device=dev)
+    _check(lib().smaq_dequant_blockvq(_ptr(idx), rows, nb, bd, nc, _ptr(dec), _ptr(out), _stream(dev)),
+           "smaq_dequant_blockvq")
+    return out
+
+
+# ------------------------------------------------------------- attention ---
+
+def attn_workspace_bytes(p: AttnParams) -> int:
+    n = lib().smaq_attn_workspace_bytes(ctypes.byref(p))
+    if n < 0:
+        raise ValueError("invalid attention parameters")
+    return int(n)
+
+
+def attn_hybrid(p: AttnParams, device: torch.device) -> None:
+    """Launches the fused attention described by p (workspace already set)."""
+    _check(lib().smaq_attn_hybrid(ctypes.byref(p), _stream(device)), "smaq_attn_hybrid")

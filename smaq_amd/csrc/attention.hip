@@ -1,0 +1,525 @@
+// Fused quantized-KV attention (decode and prefill), flash-decoding style.
+//
+//   partial kernels : one workgroup per (context split, KV head x row tile,
+//                     sequence).  Scores against the compressed history are
+//                     computed straight from the packed bytes (scalar codes
+//                     through the centroid LUT, or block-VQ indices through the
+//                     pre-decoded centroids), an online softmax runs over each
+//                     64-token chunk, and packed values are dequantised in
+//                     registers for the weighted sum.  The exact recent window
+//                     is one more segment with its own splits.
+//   combine kernel  : merges the (m, l, o) partials of every split; history and
+//                     recent outputs are normalised by the one shared softmax
+//                     denominator, each cast to the output dtype and then
+//                     added, as compute_hybrid_attention does.
+//
+// Score arithmetic follows the reference per segment: scalar history
+// ((q_rot . c[code]) * norm) * scale, block-VQ (q . k_hat) * scale, recent
+// (q . k) * scale, all fp32.
+#include <math.h>
+
+#include "smaq_common.h"
+
+namespace smaq {
+
+constexpr int kAttnThreads = 256;
+constexpr int kChunk = 64;       // tokens per online-softmax step
+constexpr int kRowTile = 16;     // query rows per workgroup
+constexpr int kMaxHeadDim = 256;
+
+struct HistAddr {
+  const long long* seq_start;  // NULL: sequence b starts at b * uniform_len
+  long long uniform_len;
+  long long head_stride;
+  const int* table;
+  int max_blocks, block_size, n_kv;
+  __device__ __forceinline__ int64_t row(int b, int h, int64_t t) const {
+    if (table) {
+      const int blk = table[(int64_t)b * max_blocks + t / block_size];
+      return ((int64_t)blk * n_kv + h) * block_size + (t % block_size);
+    }
+    return (int64_t)h * head_stride + (seq_start ? seq_start[b] : (int64_t)b * uniform_len) + t;
+  }
+};
+
+struct Partials {
+  float* m;  // [B][Hkv][rows][S]
+  float* l;
+  float* o;  // [B][Hkv][rows][S][D]
+  int S;
+  __device__ __forceinline__ int64_t idx(int b, int h, int nkv, int rows, int r, int s) const {
+    return (((int64_t)b * nkv + h) * rows + r) * S + s;
+  }
+};
+
+struct Seg {
+  int64_t t0, t1;  // token range of this split inside the sequence
+};
+
+// Online softmax over one chunk of scores already in sc[r][0..kChunk).
+__device__ __forceinline__ void softmax_chunk(float (*sc)[kChunk], float* m_s, float* l_s,
+                                              float* alpha_s, int nr) {
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (int r = w; r < nr; r += kAttnThreads / 64) {
+    const float s = sc[r][lane];
+    const float cm = warp_max(s);
+    const float m_old = m_s[r];
+    const float m_new = fmaxf(m_old, cm);
+    const float p = (m_new == -__builtin_inff()) ? 0.0f : __expf(s - m_new);
+    const float alpha = (m_old == -__builtin_inff()) ? 0.0f : __expf(m_old - m_new);
+    const float ls = warp_sum(p);
+    sc[r][lane] = p;
+    if (lane == 0) {
+      l_s[r] = l_s[r] * alpha + ls;
+      m_s[r] = m_new;
+      alpha_s[r] = alpha;
+    }
+  }
+}
+
+// ------------------------------------------------------------ history ------
+template <int KEY, typename TN, typename TV>
+__global__ __launch_bounds__(kAttnThreads) void attn_hist_kernel(smaq_attn_params p, HistAddr addr,
+                                                                 Partials part, int64_t split_len,
+                                                                 int row_tiles) {
+  __shared__ float qs[kRowTile][kMaxHeadDim];
+  __shared__ float sc[kRowTile][kChunk];
+  __shared__ float m_s[kRowTile], l_s[kRowTile], alpha_s[kRowTile];
+  __shared__ long long qpos[kRowTile];
+  __shared__ int64_t rowaddr[kChunk];
+  __shared__ float lut[256];
+
+  const int D = p.head_dim;
+  const int g = p.n_q_heads / p.n_kv_heads;
+  const int rows = p.q_len * g;
+  const int s = blockIdx.x;
+  const int h = blockIdx.y / row_tiles;
+  const int rt = blockIdx.y - h * row_tiles;
+  const int b = blockIdx.z;
+  const int r0 = rt * kRowTile;
+  const int nr = min(kRowTile, rows - r0);
+  const int tid = threadIdx.x;
+  const int64_t len = p.hist_len ? min((int64_t)p.hist_len[b], (int64_t)p.max_hist_len) : p.max_hist_len;
+  const int64_t t0 = (int64_t)s * split_len;
+  const int64_t t1 = min(len, t0 + split_len);
+
+  for (int i = tid; i < nr * D; i += kAttnThreads) {
+    const int r = i / D, d = i - r * D;
+    const int row = r0 + r, t = row / g, j = row - t * g;
+    qs[r][d] = p.q_hist[(((int64_t)b * p.q_len + t) * p.n_q_heads + h * g + j) * D + d];
+  }
+  if (tid < nr) {
+    m_s[tid] = -__builtin_inff();
+    l_s[tid] = 0.0f;
+    const int t = (r0 + tid) / g;
+    qpos[tid] = p.q_positions ? p.q_positions[(int64_t)b * p.q_len + t] : 0;
+  }
+  if (KEY == SMAQ_KEY_SCALAR) {
+    for (int i = tid; i < (1 << p.key_bits); i += kAttnThreads) lut[i] = p.key_lut[i];
+  }
+
+  // PV mapping: thread owns dim pd and rows pr0, pr0 + prs, ...
+  const int prs = kAttnThreads / D;
+  const int pd = tid % D, pr0 = tid / D;
+  float o[kRowTile];
+#pragma unroll
+  for (int i = 0; i < kRowTile; ++i) o[i] = 0.0f;
+
+  // score mapping: thread owns token st and rows sr0, sr0 + 4, ...
+  const int st = tid % kChunk, sr0 = tid / kChunk;
+  const int kbits = p.key_bits;
+  const int kvpb = (8 / kbits) > 1 ? 8 / kbits : 1;
+  const uint32_t kmask = (1u << kbits) - 1u;
+  const int vbits = p.val_bits;
+  const int vvpb = vbits == 2 ? 4 : (vbits == 4 ? 2 : 1);
+  const uint32_t vmask = (1u << vbits) - 1u;
+  const int ng = D / p.val_group;
+  const uint8_t* kbytes = (const uint8_t*)p.key_bytes;
+  const uint8_t* vbytes = (const uint8_t*)p.val_bytes;
+  const TV* vsc = (const TV*)p.val_scales;
+  const TV* vz = (const TV*)p.val_zeros;
+  __syncthreads();
+
+  for (int64_t c0 = t0; c0 < t1; c0 += kChunk) {
+    // ---- scores
+    const int64_t t = c0 + st;
+    const bool valid = t < t1;
+    int64_t ra = 0;
+    if (valid) ra = addr.row(b, h, t);
+    if (sr0 == 0) rowaddr[st] = ra;
+    float acc[kRowTile / 4];
+#pragma unroll
+    for (int i = 0; i < kRowTile / 4; ++i) acc[i] = 0.0f;
+    if (valid) {
+      const uint8_t* kr = kbytes + ra * p.key_row_bytes;
+      if (KEY == SMAQ_KEY_SCALAR) {
+        for (int d = 0; d < D; ++d) {
+          const uint32_t byte = kr[d / kvpb];
+          const float kv = lut[(byte >> ((d % kvpb) * kbits)) & kmask];
+#pragma unroll
+          for (int i = 0; i < kRowTile / 4; ++i) {
+            const int r = sr0 + 4 * i;
+            if (r < nr) acc[i] = fmaf(qs[r][d], kv, acc[i]);
+          }
+        }
+      } else {
+        const int bd = p.vq_block_dim, nc = p.vq_centroids;
+        for (int blk = 0; blk < p.vq_blocks; ++blk) {
+          const int ci = min((int)kr[blk], nc - 1);
+          const float* cent = p.key_lut + ((int64_t)blk * nc + ci) * bd;
+          for (int e = 0; e < bd; ++e) {
+            const float kv = cent[e];
+            const int d = blk * bd + e;
+#pragma unroll
+            for (int i = 0; i < kRowTile / 4; ++i) {
+              const int r = sr0 + 4 * i;
+              if (r < nr) acc[i] = fmaf(qs[r][d], kv, acc[i]);
+            }
+          }
+        }
+      }
+    }
+    const float nrm = (KEY == SMAQ_KEY_SCALAR && valid) ? Num<TN>::to_f(((const TN*)p.key_norms)[ra]) : 1.0f;
+#pragma unroll
+    for (int i = 0; i < kRowTile / 4; ++i) {
+      const int r = sr0 + 4 * i;
+      if (r < nr) {
+        float sv = (KEY == SMAQ_KEY_SCALAR) ? (acc[i] * nrm) * p.scale : acc[i] * p.scale;
+        if (!valid) sv = -__builtin_inff();
+        if (p.q_positions && valid && p.hist_pos_offset + t > qpos[r]) sv = -__builtin_inff();
+        sc[r][st] = sv;
+      }
+    }
+    __syncthreads();
+    softmax_chunk(sc, m_s, l_s, alpha_s, nr);
+    __syncthreads();
+    // ---- weighted values
+    const int nt = (int)min((int64_t)kChunk, t1 - c0);
+#pragma unroll
+    for (int i = 0; i < kRowTile; ++i) {
+      const int r = pr0 + i * prs;
+      if (i * prs < kRowTile && r < nr && pr0 < prs) o[i] *= alpha_s[r];
+    }
+    if (pr0 < prs) {
+      for (int k = 0; k < nt; ++k) {
+        const int64_t va = rowaddr[k];
+        const uint32_t byte = vbytes[va * p.val_row_bytes + pd / vvpb];
+        const uint32_t code = (vvpb == 1) ? byte : (byte >> ((pd % vvpb) * vbits)) & vmask;
+        const int gi = pd / p.val_group;
+        const float vhat = (float)code * Num<TV>::to_f(vsc[va * ng + gi]) + Num<TV>::to_f(vz[va * ng + gi]);
+#pragma unroll
+        for (int i = 0; i < kRowTile; ++i) {
+          const int r = pr0 + i * prs;
+          if (i * prs < kRowTile && r < nr) o[i] = fmaf(sc[r][k], vhat, o[i]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+  // ---- write partials
+  if (pr0 < prs) {
+#pragma unroll
+    for (int i = 0; i < kRowTile; ++i) {
+      const int r = pr0 + i * prs;
+      if (i * prs < kRowTile && r < nr) {
+        const int64_t pi = part.idx(b, h, p.n_kv_heads, rows, r0 + r, s);
+        part.o[pi * D + pd] = o[i];
+      }
+    }
+  }
+  if (tid < nr) {
+    const int64_t pi = part.idx(b, h, p.n_kv_heads, rows, r0 + tid, s);
+    part.m[pi] = m_s[tid];
+    part.l[pi] = l_s[tid];
+  }
+}
+
+// ------------------------------------------------------------- recent ------
+template <typename TR>
+__global__ __launch_bounds__(kAttnThreads) void attn_recent_kernel(smaq_attn_params p, Partials part,
+                                                                   int s_base, int64_t split_len,
+                                                                   int row_tiles) {
+  __shared__ float qs[kRowTile][kMaxHeadDim];
+  __shared__ float sc[kRowTile][kChunk];
+  __shared__ float m_s[kRowTile], l_s[kRowTile], alpha_s[kRowTile];
+  __shared__ long long qpos[kRowTile];
+
+  const int D = p.head_dim;
+  const int g = p.n_q_heads / p.n_kv_heads;
+  const int rows = p.q_len * g;
+  const int s = blockIdx.x;
+  const int h = blockIdx.y / row_tiles;
+  const int rt = blockIdx.y - h * row_tiles;
+  const int b = blockIdx.z;
+  const int r0 = rt * kRowTile;
+  const int nr = min(kRowTile, rows - r0);
+  const int tid = threadIdx.x;
+  const int64_t len = p.recent_len ? min((int64_t)p.recent_len[b], (int64_t)p.max_recent_len) : p.max_recent_len;
+  const int64_t t0 = (int64_t)s * split_len;
+  const int64_t t1 = min(len, t0 + split_len);
+  const TR* rk = (const TR*)p.recent_k + (int64_t)b * p.recent_batch_stride;
+  const TR* rv = (const TR*)p.recent_v + (int64_t)b * p.recent_batch_stride;
+  const int64_t tstride = (int64_t)p.n_kv_heads * D;
+
+  for (int i = tid; i < nr * D; i += kAttnThreads) {
+    const int r = i / D, d = i - r * D;
+    const int row = r0 + r, t = row / g, j = row - t * g;
+    qs[r][d] = p.q_exact[(((int64_t)b * p.q_len + t) * p.n_q_heads + h * g + j) * D + d];
+  }
+  if (tid < nr) {
+    m_s[tid] = -__builtin_inff();
+    l_s[tid] = 0.0f;
+    const int t = (r0 + tid) / g;
+    qpos[tid] = p.q_positions ? p.q_positions[(int64_t)b * p.q_len + t] : 0;
+  }
+  const int prs = kAttnThreads / D;
+  const int pd = tid % D, pr0 = tid / D;
+  float o[kRowTile];
+#pragma unroll
+  for (int i = 0; i < kRowTile; ++i) o[i] = 0.0f;
+  const int st = tid % kChunk, sr0 = tid / kChunk;
+  __syncthreads();
+
+  for (int64_t c0 = t0; c0 < t1; c0 += kChunk) {
+    const int64_t t = c0 + st;
+    const bool valid = t < t1;
+    float acc[kRowTile / 4];
+#pragma unroll
+    for (int i = 0; i < kRowTile / 4; ++i) acc[i] = 0.0f;
+    if (valid) {
+      const TR* kr = rk + t * tstride + (int64_t)h * D;
+      for (int d = 0; d < D; ++d) {
+        const float kv = Num<TR>::to_f(kr[d]);
+#pragma unroll
+        for (int i = 0; i < kRowTile / 4; ++i) {
+          const int r = sr0 + 4 * i;
+          if (r < nr) acc[i] = fmaf(qs[r][d], kv, acc[i]);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kRowTile / 4; ++i) {
+      const int r = sr0 + 4 * i;
+      if (r < nr) {
+        float sv = valid ? acc[i] * p.scale : -__builtin_inff();
+        if (p.q_positions && valid && p.recent_pos_offset + t > qpos[r]) sv = -__builtin_inff();
+        sc[r][st] = sv;
+      }
+    }
+    __syncthreads();
+    softmax_chunk(sc, m_s, l_s, alpha_s, nr);
+    __syncthreads();
+    const int nt = (int)min((int64_t)kChunk, t1 - c0);
+#pragma unroll
+    for (int i = 0; i < kRowTile; ++i) {
+      const int r = pr0 + i * prs;
+      if (i * prs < kRowTile && r < nr && pr0 < prs) o[i] *= alpha_s[r];
+    }
+    if (pr0 < prs) {
+      for (int k = 0; k < nt; ++k) {
+        const float vv = Num<TR>::to_f(rv[(c0 + k) * tstride + (int64_t)h * D + pd]);
+#pragma unroll
+        for (int i = 0; i < kRowTile; ++i) {
+          const int r = pr0 + i * prs;
+          if (i * prs < kRowTile && r < nr) o[i] = fmaf(sc[r][k], vv, o[i]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (pr0 < prs) {
+#pragma unroll
+    for (int i = 0; i < kRowTile; ++i) {
+      const int r = pr0 + i * prs;
+      if (i * prs < kRowTile && r < nr) {
+        const int64_t pi = part.idx(b, h, p.n_kv_heads, rows, r0 + r, s_base + s);
+        part.o[pi * D + pd] = o[i];
+      }
+    }
+  }
+  if (tid < nr) {
+    const int64_t pi = part.idx(b, h, p.n_kv_heads, rows, r0 + tid, s_base + s);
+    part.m[pi] = m_s[tid];
+    part.l[pi] = l_s[tid];
+  }
+}
+
+// ------------------------------------------------------------ combine ------
+template <typename TO>
+__global__ __launch_bounds__(kMaxHeadDim) void attn_combine_kernel(smaq_attn_params p, Partials part,
+                                                                   int s_hist) {
+  const int D = p.head_dim;
+  const int g = p.n_q_heads / p.n_kv_heads;
+  const int rows = p.q_len * g;
+  const int r = blockIdx.x;   // row within the KV head group
+  const int h = blockIdx.y;
+  const int b = blockIdx.z;
+  const int d = threadIdx.x;
+  if (d >= D) return;
+  const int64_t base = part.idx(b, h, p.n_kv_heads, rows, r, 0);
+  float M = -__builtin_inff();
+  for (int s = 0; s < part.S; ++s)
+    if (part.l[base + s] > 0.0f) M = fmaxf(M, part.m[base + s]);
+  float L = 0.0f, oh = 0.0f, orc = 0.0f;
+  for (int s = 0; s < part.S; ++s) {
+    const float l = part.l[base + s];
+    if (!(l > 0.0f)) continue;
+    const float w = __expf(part.m[base + s] - M);
+    L = fmaf(l, w, L);
+    const float v = part.o[(base + s) * D + d] * w;
+    if (s < s_hist) oh += v; else orc += v;
+  }
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+  oh *= inv;
+  orc *= inv;
+  float res;
+  if (p.has_history && p.has_recent) res = Num<TO>::round(Num<TO>::round(oh) + Num<TO>::round(orc));
+  else res = p.has_history ? oh : orc;
+  const int t = r / g, j = r - t * g;
+  ((TO*)p.out)[(((int64_t)b * p.q_len + t) * p.n_q_heads + h * g + j) * D + d] = Num<TO>::from_f(res);
+}
+
+struct Plan {
+  int row_tiles;
+  int64_t hist_split, recent_split;
+  int s_hist, s_recent;
+};
+
+static Plan make_plan(const smaq_attn_params* p) {
+  Plan pl;
+  const int g = p->n_q_heads / p->n_kv_heads;
+  const int rows = p->q_len * g;
+  pl.row_tiles = (rows + kRowTile - 1) / kRowTile;
+  const int64_t units = (int64_t)p->batch * p->n_kv_heads * pl.row_tiles;
+  // aim for >= 2048 workgroups over the history
+  int64_t want = units >= 2048 ? 1 : (2048 + units - 1) / units;
+  int64_t hl = p->has_history ? p->max_hist_len : 0;
+  int64_t split = hl > 0 ? (hl + want - 1) / want : kChunk;
+  split = ((split + kChunk - 1) / kChunk) * kChunk;
+  if (split < 4 * kChunk) split = 4 * kChunk;
+  pl.hist_split = split;
+  pl.s_hist = hl > 0 ? (int)((hl + split - 1) / split) : 0;
+  int64_t rl = p->has_recent ? p->max_recent_len : 0;
+  pl.recent_split = 4 * kChunk;
+  pl.s_recent = rl > 0 ? (int)((rl + pl.recent_split - 1) / pl.recent_split) : 0;
+  return pl;
+}
+
+}  // namespace smaq
+
+using namespace smaq;
+
+extern "C" long long smaq_attn_workspace_bytes(const smaq_attn_params* p) {
+  if (!p || p->n_kv_heads <= 0 || p->n_q_heads % p->n_kv_heads) return -1;
+  const Plan pl = make_plan(p);
+  const int64_t S = pl.s_hist + pl.s_recent;
+  const int64_t rows = (int64_t)p->q_len * (p->n_q_heads / p->n_kv_heads);
+  const int64_t n = (int64_t)p->batch * p->n_kv_heads * rows * (S > 0 ? S : 1);
+  return n * (p->head_dim + 2) * (long long)sizeof(float);
+}
+
+template <int KEY, typename TN, typename TV>
+static void launch_hist(const smaq_attn_params& p, const HistAddr& a, const Partials& part,
+                        const Plan& pl, hipStream_t st) {
+  dim3 grid(pl.s_hist, p.n_kv_heads * pl.row_tiles, p.batch);
+  hipLaunchKernelGGL((attn_hist_kernel<KEY, TN, TV>), grid, dim3(kAttnThreads), 0, st, p, a, part,
+                     pl.hist_split, pl.row_tiles);
+}
+
+template <int KEY, typename TN>
+static int dispatch_hist_v(const smaq_attn_params& p, const HistAddr& a, const Partials& part,
+                           const Plan& pl, hipStream_t st) {
+  switch (p.val_dtype) {
+    case SMAQ_F32: launch_hist<KEY, TN, float>(p, a, part, pl, st); return SMAQ_OK;
+    case SMAQ_F16: launch_hist<KEY, TN, _Float16>(p, a, part, pl, st); return SMAQ_OK;
+    case SMAQ_BF16: launch_hist<KEY, TN, bf16>(p, a, part, pl, st); return SMAQ_OK;
+  }
+  set_error("smaq_attn_hybrid: unsupported value dtype %d", p.val_dtype);
+  return SMAQ_EUNSUPPORTED;
+}
+
+extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
+  SMAQ_REQUIRE(pp, "smaq_attn_hybrid: null params");
+  const smaq_attn_params& p = *pp;
+  hipStream_t st = (hipStream_t)stream;
+  SMAQ_REQUIRE(p.batch > 0 && p.q_len > 0 && p.n_kv_heads > 0 && p.n_q_heads > 0,
+               "smaq_attn_hybrid: empty shape");
+  SMAQ_REQUIRE(p.n_q_heads % p.n_kv_heads == 0, "smaq_attn_hybrid: Hq %% Hkv != 0");
+  SMAQ_REQUIRE(p.head_dim > 0 && p.head_dim <= kMaxHeadDim && kAttnThreads % p.head_dim == 0,
+               "smaq_attn_hybrid: head_dim %d unsupported (must divide 256)", p.head_dim);
+  SMAQ_REQUIRE(p.batch < 65536 && (int64_t)p.n_kv_heads * ((p.q_len * (p.n_q_heads / p.n_kv_heads) + kRowTile - 1) / kRowTile) < 65536,
+               "smaq_attn_hybrid: grid too large");
+  SMAQ_REQUIRE(p.out && p.workspace, "smaq_attn_hybrid: null output/workspace");
+  SMAQ_REQUIRE(p.has_history || p.has_recent, "smaq_attn_hybrid: nothing to attend");
+  if (p.has_history) {
+    SMAQ_REQUIRE(p.q_hist && p.key_bytes && p.key_lut && p.val_bytes && p.val_scales && p.val_zeros,
+                 "smaq_attn_hybrid: null history pointer");
+    SMAQ_REQUIRE(p.val_group > 0 && p.head_dim % p.val_group == 0, "smaq_attn_hybrid: bad value group");
+    SMAQ_REQUIRE(p.val_bits >= 1 && p.val_bits <= 8, "smaq_attn_hybrid: bad value bits");
+    if (p.block_table) SMAQ_REQUIRE(p.block_size > 0 && p.max_blocks > 0, "smaq_attn_hybrid: bad paging");
+    if (p.key_format == SMAQ_KEY_SCALAR) {
+      SMAQ_REQUIRE(p.key_bits >= 1 && p.key_bits <= 8 && p.key_norms, "smaq_attn_hybrid: bad scalar keys");
+    } else {
+      SMAQ_REQUIRE(p.key_format == SMAQ_KEY_BLOCKVQ && p.vq_blocks * p.vq_block_dim == p.head_dim &&
+                       p.vq_centroids >= 1 && p.vq_centroids <= 256,
+                   "smaq_attn_hybrid: bad block-VQ keys");
+    }
+    SMAQ_REQUIRE(p.max_hist_len > 0, "smaq_attn_hybrid: history without tokens");
+  }
+  if (p.has_recent) {
+    SMAQ_REQUIRE(p.q_exact && p.recent_k && p.recent_v && p.max_recent_len > 0,
+                 "smaq_attn_hybrid: null recent pointer");
+  }
+  const Plan pl = make_plan(&p);
+  const long long need = smaq_attn_workspace_bytes(&p);
+  SMAQ_REQUIRE(p.workspace_bytes >= need, "smaq_attn_hybrid: workspace %lld < %lld bytes",
+               p.workspace_bytes, need);
+  const int S = pl.s_hist + pl.s_recent;
+  const int g = p.n_q_heads / p.n_kv_heads;
+  const int64_t rows = (int64_t)p.q_len * g;
+  const int64_t n_part = (int64_t)p.batch * p.n_kv_heads * rows * S;
+  Partials part;
+  part.S = S;
+  part.m = (float*)p.workspace;
+  part.l = part.m + n_part;
+  part.o = part.l + n_part;
+
+  const int phases = p.phases ? p.phases : 7;
+  if (pl.s_hist > 0 && (phases & 1)) {
+    HistAddr a{p.hist_seq_start, p.max_hist_len, p.hist_head_stride, p.block_table, p.max_blocks,
+               p.block_size, p.n_kv_heads};
+    int rc = SMAQ_EUNSUPPORTED;
+    if (p.key_format == SMAQ_KEY_SCALAR) {
+      switch (p.norm_dtype) {
+        case SMAQ_F32: rc = dispatch_hist_v<SMAQ_KEY_SCALAR, float>(p, a, part, pl, st); break;
+        case SMAQ_F16: rc = dispatch_hist_v<SMAQ_KEY_SCALAR, _Float16>(p, a, part, pl, st); break;
+        case SMAQ_BF16: rc = dispatch_hist_v<SMAQ_KEY_SCALAR, bf16>(p, a, part, pl, st); break;
+        default: set_error("smaq_attn_hybrid: unsupported norm dtype %d", p.norm_dtype);
+      }
+    } else {
+      rc = dispatch_hist_v<SMAQ_KEY_BLOCKVQ, float>(p, a, part, pl, st);
+    }
+    if (rc != SMAQ_OK) return rc;
+    if ((rc = launch_status("smaq_attn_hybrid(history)")) != SMAQ_OK) return rc;
+  }
+  if (pl.s_recent > 0 && (phases & 2)) {
+    dim3 grid(pl.s_recent, p.n_kv_heads * pl.row_tiles, p.batch);
+    switch (p.recent_dtype) {
+      case SMAQ_F32: hipLaunchKernelGGL(attn_recent_kernel<float>, grid, dim3(kAttnThreads), 0, st, p, part, pl.s_hist, pl.recent_split, pl.row_tiles); break;
+      case SMAQ_F16: hipLaunchKernelGGL(attn_recent_kernel<_Float16>, grid, dim3(kAttnThreads), 0, st, p, part, pl.s_hist, pl.recent_split, pl.row_tiles); break;
+      case SMAQ_BF16: hipLaunchKernelGGL(attn_recent_kernel<bf16>, grid, dim3(kAttnThreads), 0, st, p, part, pl.s_hist, pl.recent_split, pl.row_tiles); break;
+      default: set_error("smaq_attn_hybrid: unsupported recent dtype %d", p.recent_dtype); return SMAQ_EUNSUPPORTED;
+    }
+    const int rc = launch_status("smaq_attn_hybrid(recent)");
+    if (rc != SMAQ_OK) return rc;
+  }
+  if (!(phases & 4)) return SMAQ_OK;
+  dim3 cgrid((unsigned)rows, p.n_kv_heads, p.batch);
+  switch (p.out_dtype) {
+    case SMAQ_F32: hipLaunchKernelGGL(attn_combine_kernel<float>, cgrid, dim3(kMaxHeadDim), 0, st, p, part, pl.s_hist); break;
+    case SMAQ_F16: hipLaunchKernelGGL(attn_combine_kernel<_Float16>, cgrid, dim3(kMaxHeadDim), 0, st, p, part, pl.s_hist); break;
+    case SMAQ_BF16: hipLaunchKernelGGL(attn_combine_kernel<bf16>, cgrid, dim3(kMaxHeadDim), 0, st, p, part, pl.s_hist); break;
+    default: set_error("smaq_attn_hybrid: unsupported output dtype %d", p.out_dtype); return SMAQ_EUNSUPPORTED;
+  }
+  return launch_status("smaq_attn_hybrid(combine)");
+}

@@ -1,0 +1,155 @@
+// Value codec: groupwise asymmetric min/max quantisation (the value bit-packer)
+// and its dequantiser.
+//
+// Bit-exactness: every elementwise op is rounded to the value dtype, as
+// torch-CPU does for bf16/fp16 tensors (compute in fp32, round once, RNE):
+//   range = rnd(max - min); scale = rnd(range / levels)  (true division)
+//   scale = max(scale, rnd(1e-10))  -- clamp bound converted to the dtype
+//   code  = clamp(rint(rnd(rnd(v - min) / scale)), 0, levels), NaN -> 0
+#include "smaq_common.h"
+
+namespace smaq {
+
+// Codes stored per byte: 2-bit -> 4, 4-bit -> 2, other widths unpacked.
+__host__ __device__ __forceinline__ int value_codes_per_byte(int bits) {
+  return bits == 2 ? 4 : (bits == 4 ? 2 : 1);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void pack_values_kernel(
+    const T* __restrict__ v, RowMap map, int64_t rows, int D, int bits, int group,
+    int groups_per_thread, uint8_t* __restrict__ data, T* __restrict__ scales,
+    T* __restrict__ zeros) {
+  const int n_groups = D / group;
+  const int units_per_row = n_groups / groups_per_thread;
+  const int64_t unit = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (unit >= rows * units_per_row) return;
+  const int64_t row = unit / units_per_row;
+  const int g0 = (int)(unit - row * units_per_row) * groups_per_thread;
+  const T* src = v + map.offset(row);
+  const int vpb = value_codes_per_byte(bits);
+  const int row_bytes = D / vpb;
+  const float levels = (float)((1 << bits) - 1);
+  const float min_scale = dtype_const<T>(1e-10f);
+
+  uint32_t acc = 0;  // byte under construction
+  int filled = 0;
+  for (int g = g0; g < g0 + groups_per_thread; ++g) {
+    const T* gp = src + (int64_t)g * group;
+    float lo = Num<T>::to_f(gp[0]);
+    float hi = lo;
+    for (int e = 1; e < group; ++e) {
+      const float x = Num<T>::to_f(gp[e]);
+      lo = fminf(lo, x);
+      hi = fmaxf(hi, x);
+    }
+    float sc = Num<T>::round(Num<T>::round(hi - lo) / levels);
+    if (sc < min_scale) sc = min_scale;  // clamp(min=1e-10), NaN passes
+    scales[row * n_groups + g] = Num<T>::from_f(sc);
+    zeros[row * n_groups + g] = Num<T>::from_f(lo);
+    for (int e = 0; e < group; ++e) {
+      const float x = Num<T>::to_f(gp[e]);
+      float q = round_half_even(Num<T>::round(Num<T>::round(x - lo) / sc));
+      q = fminf(fmaxf(q, 0.0f), levels);
+      const uint32_t code = (q == q) ? (uint32_t)q : 0u;  // NaN -> 0
+      acc |= code << (filled * bits);
+      if (++filled == vpb) {
+        const int d = g * group + e;
+        data[row * row_bytes + d / vpb] = (uint8_t)acc;
+        acc = 0;
+        filled = 0;
+      }
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void dequant_values_kernel(
+    const uint8_t* __restrict__ data, const T* __restrict__ scales, const T* __restrict__ zeros,
+    int64_t rows, int D, int bits, int group, float* __restrict__ out) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= rows * D) return;
+  const int64_t row = idx / D;
+  const int d = (int)(idx - row * D);
+  const int vpb = value_codes_per_byte(bits);
+  const int row_bytes = D / vpb;
+  const uint32_t byte = data[row * row_bytes + d / vpb];
+  const uint32_t code = (vpb == 1) ? byte : (byte >> ((d % vpb) * bits)) & ((1u << bits) - 1u);
+  const int n_groups = D / group;
+  const float s = Num<T>::to_f(scales[row * n_groups + d / group]);
+  const float z = Num<T>::to_f(zeros[row * n_groups + d / group]);
+  out[idx] = (float)code * s + z;  // two roundings (fp-contract off), as torch
+}
+
+template <typename T>
+static int launch_pack(const void* v, RowMap map, int64_t rows, int D, int bits, int group,
+                       void* data, void* scales, void* zeros, hipStream_t stream) {
+  const int vpb = value_codes_per_byte(bits);
+  const int gpt = (group % vpb == 0) ? 1 : D / group;  // bytes straddle groups
+  const int64_t units = rows * ((D / group) / gpt);
+  const int threads = 256;
+  const int64_t blocks = (units + threads - 1) / threads;
+  hipLaunchKernelGGL(pack_values_kernel<T>, dim3((unsigned)blocks), dim3(threads), 0, stream,
+                     (const T*)v, map, rows, D, bits, group, gpt, (uint8_t*)data, (T*)scales,
+                     (T*)zeros);
+  return launch_status("smaq_pack_values");
+}
+
+template <typename T>
+static int launch_dequant(const void* data, const void* scales, const void* zeros, int64_t rows,
+                          int D, int bits, int group, float* out, hipStream_t stream) {
+  const int64_t n = rows * D;
+  const int threads = 256;
+  hipLaunchKernelGGL(dequant_values_kernel<T>, dim3((unsigned)((n + threads - 1) / threads)),
+                     dim3(threads), 0, stream, (const uint8_t*)data, (const T*)scales,
+                     (const T*)zeros, rows, D, bits, group, out);
+  return launch_status("smaq_dequant_values");
+}
+
+}  // namespace smaq
+
+using namespace smaq;
+
+extern "C" int smaq_pack_values(const void* v, int vdtype, long long n_outer, long long n_inner,
+                                long long s_outer, long long s_inner, int D, int bits, int group,
+                                void* data_out, void* scales_out, void* zeros_out, void* stream) {
+  SMAQ_REQUIRE(v && data_out && scales_out && zeros_out, "smaq_pack_values: null pointer");
+  SMAQ_REQUIRE(D > 0 && group > 0 && D % group == 0,
+               "head_dim %d must be divisible by group_size %d", D, group);
+  SMAQ_REQUIRE(bits >= 1 && bits <= 8, "smaq_pack_values: bits must be in [1, 8], got %d", bits);
+  SMAQ_REQUIRE(D % value_codes_per_byte(bits) == 0,
+               "head_dim %d must be divisible by %d for %d-bit packing", D,
+               value_codes_per_byte(bits), bits);
+  SMAQ_REQUIRE(n_outer >= 0 && n_inner > 0, "smaq_pack_values: bad row shape");
+  const int64_t rows = (int64_t)n_outer * n_inner;
+  if (rows == 0) return SMAQ_OK;
+  SMAQ_REQUIRE(rows * (D / group) < (1ll << 40), "smaq_pack_values: too many rows");
+  RowMap map{n_inner, s_outer, s_inner};
+  hipStream_t st = (hipStream_t)stream;
+  switch (vdtype) {
+    case SMAQ_F32: return launch_pack<float>(v, map, rows, D, bits, group, data_out, scales_out, zeros_out, st);
+    case SMAQ_F16: return launch_pack<_Float16>(v, map, rows, D, bits, group, data_out, scales_out, zeros_out, st);
+    case SMAQ_BF16: return launch_pack<bf16>(v, map, rows, D, bits, group, data_out, scales_out, zeros_out, st);
+  }
+  set_error("smaq_pack_values: unsupported dtype %d", vdtype);
+  return SMAQ_EUNSUPPORTED;
+}
+
+extern "C" int smaq_dequant_values(const void* data, const void* scales, const void* zeros,
+                                   int sdtype, long long rows, int D, int bits, int group,
+                                   float* out, void* stream) {
+  SMAQ_REQUIRE(data && scales && zeros && out, "smaq_dequant_values: null pointer");
+  SMAQ_REQUIRE(D > 0 && group > 0 && D % group == 0,
+               "head_dim %d must be divisible by group_size %d", D, group);
+  SMAQ_REQUIRE(bits >= 1 && bits <= 8, "smaq_dequant_values: bits must be in [1, 8]");
+  SMAQ_REQUIRE(D % value_codes_per_byte(bits) == 0, "smaq_dequant_values: bad packing");
+  if (rows <= 0) return SMAQ_OK;
+  hipStream_t st = (hipStream_t)stream;
+  switch (sdtype) {
+    case SMAQ_F32: return launch_dequant<float>(data, scales, zeros, rows, D, bits, group, out, st);
+    case SMAQ_F16: return launch_dequant<_Float16>(data, scales, zeros, rows, D, bits, group, out, st);
+    case SMAQ_BF16: return launch_dequant<bf16>(data, scales, zeros, rows, D, bits, group, out, st);
+  }
+  set_error("smaq_dequant_values: unsupported dtype %d", sdtype);
+  return SMAQ_EUNSUPPORTED;
+}

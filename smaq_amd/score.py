@@ -1,0 +1,294 @@
+"""Hybrid attention over compressed history plus exact recent tokens
+(drop-in for smaq/score.py).
+
+``compute_hybrid_attention`` keeps the reference's semantics
+(smaq/score.py:23-72): one softmax over the concatenated [history; recent]
+logits, history ignored below ``MIN_HISTORY_FOR_SMAQ`` tokens, GQA by head
+grouping, each part cast to the query dtype before the sum, zeros when there
+is nothing to attend.  For the GPU codecs it is one fused HIP launch sequence
+(scores from packed codes, online softmax, in-register value dequantisation);
+strategies without a fused description go through their own
+``attention_score`` per KV head.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+
+from smaq_amd import _native
+from smaq_amd.core import AttentionBackend
+from smaq_amd.kv_cache import dequantize_values
+from smaq_amd.store import CompressedKVStore, FlatCache
+
+MIN_HISTORY_FOR_SMAQ = 16
+
+
+class AttentionPlan:
+    """A prepared fused-attention launch.
+
+    Parameters, workspace, output and the fp32/rotated query buffers are
+    allocated once; ``run(query)`` copies the new query in and re-launches.
+    Decode loops reuse one plan per step shape, so a step costs the kernel
+    launches only.  Shapes: query [B, T, Hq, D]; history fields are
+    row-indexed per-token tensors (see include/smaq_hip.h); recent_k/v
+    [B, R, Hkv, D].
+    """
+
+    def __init__(
+        self,
+        *,
+        query: torch.Tensor,
+        fused,
+        key_codes: Optional[torch.Tensor],
+        key_norms: Optional[torch.Tensor],
+        val_data: Optional[torch.Tensor],
+        val_scales: Optional[torch.Tensor],
+        val_zeros: Optional[torch.Tensor],
+        val_bits: int,
+        val_group: int,
+        n_kv_heads: int,
+        hist_len: Optional[torch.Tensor],
+        max_hist_len: int,
+        hist_seq_start: Optional[torch.Tensor] = None,
+        hist_head_stride: int = 0,
+        block_table: Optional[torch.Tensor] = None,
+        block_size: int = 0,
+        recent_k: Optional[torch.Tensor] = None,
+        recent_v: Optional[torch.Tensor] = None,
+        recent_len: Optional[torch.Tensor] = None,
+        max_recent_len: int = 0,
+        scale: float,
+        out_dtype: torch.dtype,
+        query_positions: Optional[torch.Tensor] = None,
+        hist_pos_offset: int = 0,
+        recent_pos_offset: int = 0,
+    ):
+        dev = _native.require_gpu(query, key_codes, val_data, recent_k)
+        self.device = dev
+        B, T, Hq, D = query.shape
+        self.shape = (B, T, Hq, D)
+        self.fused = fused
+        has_hist = fused is not None and max_hist_len > 0
+        has_recent = recent_k is not None and max_recent_len > 0
+        p = _native.AttnParams()
+        p.batch, p.q_len, p.n_q_heads, p.n_kv_heads, p.head_dim = B, T, Hq, n_kv_heads, D
+        p.scale = float(scale)
+        keep = []
+        self.q_exact = torch.empty(B, T, Hq, D, dtype=torch.float32, device=dev)
+        p.q_exact = self.q_exact.data_ptr()
+        if query_positions is not None:
+            qp = query_positions.to(dev, torch.int64).contiguous()
+            keep.append(qp)
+            p.q_positions = qp.data_ptr()
+        p.hist_pos_offset = int(hist_pos_offset)
+        p.recent_pos_offset = int(recent_pos_offset)
+        self.q_hist = None
+        if has_hist:
+            if fused.rot_t is not None:
+                self.q_hist = torch.empty_like(self.q_exact)
+                self.rot_t = fused.rot_t.to(dev, torch.float32).contiguous()
+                self.rot_scale = None if fused.rot_scale is None else fused.rot_scale.to(dev, torch.float32).contiguous()
+                p.q_hist = self.q_hist.data_ptr()
+            else:
+                p.q_hist = self.q_exact.data_ptr()
+            p.has_history = 1
+            p.key_bytes = key_codes.data_ptr()
+            p.key_row_bytes = key_codes.shape[-1]
+            lut = fused.lut.to(dev, torch.float32).contiguous().reshape(-1)
+            if fused.kind == "scalar" and lut.numel() < (1 << fused.bits):
+                lut = torch.cat([lut, lut.new_zeros((1 << fused.bits) - lut.numel())])
+            keep.append(lut)
+            p.key_lut = lut.data_ptr()
+            if fused.kind == "scalar":
+                p.key_format = _native.KEY_SCALAR
+                p.key_bits = fused.bits
+                p.key_norms = key_norms.data_ptr()
+                p.norm_dtype = _native.dtype_code(key_norms.dtype)
+            else:
+                p.key_format = _native.KEY_BLOCKVQ
+                p.vq_blocks, p.vq_block_dim, p.vq_centroids = fused.n_blocks, fused.block_dim, fused.n_centroids
+            p.val_bytes = val_data.data_ptr()
+            p.val_row_bytes = val_data.shape[-1]
+            p.val_bits, p.val_group = val_bits, val_group
+            p.val_scales, p.val_zeros = val_scales.data_ptr(), val_zeros.data_ptr()
+            p.val_dtype = _native.dtype_code(val_scales.dtype)
+            p.hist_len = None if hist_len is None else hist_len.data_ptr()
+            p.hist_seq_start = None if hist_seq_start is None else hist_seq_start.data_ptr()
+            p.hist_head_stride = int(hist_head_stride)
+            if block_table is not None:
+                bt = block_table.to(dev, torch.int32).contiguous()
+                keep.append(bt)
+                p.block_table = bt.data_ptr()
+                p.max_blocks = bt.shape[-1]
+                p.block_size = int(block_size)
+            p.max_hist_len = int(max_hist_len)
+            keep += [t for t in (key_codes, key_norms, val_data, val_scales, val_zeros, hist_len, hist_seq_start)
+                     if t is not None]
+        if has_recent:
+            rk, rv = recent_k.contiguous(), recent_v.contiguous()
+            keep += [rk, rv] + ([recent_len] if recent_len is not None else [])
+            p.has_recent = 1
+            p.recent_k, p.recent_v = rk.data_ptr(), rv.data_ptr()
+            p.recent_dtype = _native.dtype_code(rk.dtype)
+            p.recent_len = None if recent_len is None else recent_len.data_ptr()
+            p.recent_batch_stride = rk.shape[1] * rk.shape[2] * rk.shape[3]
+            p.max_recent_len = int(max_recent_len)
+        self.out = torch.empty(B, T, Hq, D, dtype=out_dtype, device=dev)
+        p.out = self.out.data_ptr()
+        p.out_dtype = _native.dtype_code(out_dtype)
+        nbytes = _native.attn_workspace_bytes(p)
+        self.workspace = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=dev)
+        p.workspace = self.workspace.data_ptr()
+        p.workspace_bytes = self.workspace.numel()
+        self.params = p
+        self._keep = keep
+
+    def load_query(self, query: torch.Tensor) -> None:
+        """Copy a query in and prepare the codec-space query (rotate kernel)."""
+        self.q_exact.copy_(query.reshape(self.shape))
+        if self.q_hist is not None:
+            _native.rotate_rows_into(self.q_exact, self.rot_t, self.rot_scale, self.q_hist)
+
+    def launch(self, phases: int = 0) -> torch.Tensor:
+        """Launch the attention phases (0 = all) on the current stream."""
+        self.params.phases = phases
+        _native.attn_hybrid(self.params, self.device)
+        return self.out
+
+    def run(self, query: torch.Tensor) -> torch.Tensor:
+        self.load_query(query)
+        return self.launch()
+
+
+def launch_fused_attention(*, query: torch.Tensor, **kw) -> torch.Tensor:
+    """One-shot fused attention; returns [B, T, Hq, D] in out_dtype."""
+    return AttentionPlan(query=query, **kw).run(query)
+
+
+def _head_stride_rows(t: torch.Tensor):
+    """Rows between KV heads of a [Hkv, N, *tail] per-token tensor whose rows
+    are dense, or None if its rows are not laid out that way."""
+    per_row = 1
+    for s in t.shape[2:]:
+        per_row *= s
+    dense_rows = t.stride(1) == per_row and (t.dim() == 2 or t[0, 0].is_contiguous())
+    if not dense_rows or t.stride(0) % per_row:
+        return None
+    return t.stride(0) // per_row
+
+
+def _flat_tensors(flat: FlatCache):
+    """The FlatCache's per-token tensors plus their common head stride in rows
+    (copied to contiguous tensors when the views disagree)."""
+    kq, vq = flat.key_q, flat.value_q
+    norms = getattr(kq, "norms", None)
+    tensors = [kq.indices, norms, vq.data, vq.scales, vq.zeros]
+    strides = {_head_stride_rows(t) for t in tensors if t is not None}
+    if len(strides) == 1 and None not in strides:
+        return tensors, strides.pop()
+    return [None if t is None else t.contiguous() for t in tensors], flat.num_tokens
+
+
+def compute_hybrid_attention(
+    query: torch.Tensor,
+    store: CompressedKVStore,
+    recent_k: Optional[torch.Tensor],
+    recent_v: Optional[torch.Tensor],
+    num_query_heads: int,
+    scale: Optional[float] = None,
+    query_positions: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Attention of query [T, Hq, D] over the store's history and the exact
+    recent window [R, Hkv, D] (smaq/score.py:23-72).
+
+    ``query_positions`` (int64 [T], optional) is an extension for chunked
+    prefill: key j (history positions 0..N-1, then recent N..N+R-1) is visible
+    to query t iff j <= query_positions[t].  None reproduces the reference,
+    which applies no mask.
+    """
+    head_dim = store.head_dim
+    hkv = store.num_kv_heads
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim)
+    flat = store.get_flat_cache()
+    has_history = flat is not None and flat.num_tokens >= MIN_HISTORY_FOR_SMAQ
+    has_recent = recent_k is not None and recent_k.shape[0] > 0
+    if not has_history and not has_recent:
+        return torch.zeros(query.shape[0], num_query_heads, head_dim, device=query.device, dtype=query.dtype)
+    if num_query_heads % hkv:
+        raise ValueError(f"num_query_heads {num_query_heads} not a multiple of num_kv_heads {hkv}")
+    fused = None
+    if has_history:
+        fh = getattr(store.quantizer, "fused_history", None)
+        fused = fh() if fh is not None else None
+        if fused is None:
+            return _generic_hybrid(query, store, flat, recent_k, recent_v, num_query_heads, scale,
+                                   has_recent, query_positions)
+    n_all = flat.num_tokens if flat is not None else 0
+    kw = {}
+    if has_history:
+        (codes, norms, vdata, vsc, vz), stride = _flat_tensors(flat)
+        kw = dict(key_codes=codes, key_norms=norms, val_data=vdata, val_scales=vsc, val_zeros=vz,
+                  hist_head_stride=stride, max_hist_len=flat.num_tokens)
+    else:
+        kw = dict(key_codes=None, key_norms=None, val_data=None, val_scales=None, val_zeros=None,
+                  max_hist_len=0)
+    out = launch_fused_attention(
+        query=query.unsqueeze(0), fused=fused, val_bits=store.value_bits, val_group=store.value_group_size,
+        n_kv_heads=hkv, hist_len=None,
+        recent_k=recent_k.unsqueeze(0) if has_recent else None,
+        recent_v=recent_v.unsqueeze(0) if has_recent else None,
+        recent_len=None, max_recent_len=recent_k.shape[0] if has_recent else 0,
+        scale=scale, out_dtype=query.dtype,
+        query_positions=None if query_positions is None else query_positions.reshape(1, -1),
+        hist_pos_offset=0, recent_pos_offset=n_all, **kw)
+    return out.squeeze(0)
+
+
+def _generic_hybrid(query, store, flat, recent_k, recent_v, num_query_heads, scale, has_recent,
+                    query_positions):
+    """Strategies without a fused kernel description: the reference's per-head
+    composition (smaq/score.py:61-72,75-124) in GPU tensor ops."""
+    hkv = store.num_kv_heads
+    g = num_query_heads // hkv
+    T, D = query.shape[0], query.shape[-1]
+    q = query.float().view(T, hkv, g, D).permute(1, 2, 0, 3)
+    kwargs = {"use_kernel": True} if getattr(store.quantizer, "supports_kernel", False) else {}
+    per_head = [store.quantizer.attention_score(q[h], store.quantizer.select_head(flat.key_q, h), scale=scale,
+                                                **kwargs) for h in range(hkv)]
+    parts = [torch.stack(per_head, 0).permute(2, 0, 1, 3).reshape(T, num_query_heads, flat.num_tokens)]
+    if has_recent:
+        k = recent_k.transpose(0, 1).float().unsqueeze(1)
+        s = torch.matmul(q, k.transpose(-2, -1).contiguous()) * scale
+        parts.append(s.permute(2, 0, 1, 3).reshape(T, num_query_heads, recent_k.shape[0]))
+    logits = torch.cat(parts, dim=-1)
+    if query_positions is not None:
+        pos = torch.arange(logits.shape[-1], device=logits.device)
+        logits = logits.masked_fill((pos[None, :] > query_positions.to(logits.device)[:, None])[:, None, :],
+                                    float("-inf"))
+    w = F.softmax(logits, dim=-1)
+
+    def apply(weights, values):
+        v = values.float().unsqueeze(1)
+        wv = weights.float().view(T, hkv, g, weights.shape[-1]).permute(1, 2, 0, 3)
+        o = torch.matmul(wv, v)
+        return o.permute(2, 0, 1, 3).reshape(T, num_query_heads, D).to(query.dtype)
+
+    n = flat.num_tokens
+    o_h = apply(w[..., :n], dequantize_values(flat.value_q, store.value_group_size))
+    if not has_recent:
+        return o_h
+    return o_h + apply(w[..., n:], recent_v.transpose(0, 1))
+
+
+class HybridAttentionBackend(AttentionBackend):
+    """Attention backend over compressed history and exact tail
+    (smaq/score.py:141-160)."""
+
+    def compute(self, query, store, recent_k, recent_v, num_query_heads, scale: Optional[float] = None):
+        return compute_hybrid_attention(query=query, store=store, recent_k=recent_k, recent_v=recent_v,
+                                        num_query_heads=num_query_heads, scale=scale)

@@ -10,7 +10,7 @@ pass of one layer over the whole batch, cache resident in HBM.
     python bench.py [--steps K] [--warmup W] [--workload decode|encode|paged]
 
 Prints ONE JSON line.  ``value`` is decode tokens/s (batch / step time);
-``roofline`` is the dominant kernel (history partial-attention) timed with HIP
+``roofline`` is the dominant kernel (decode_mfma_kernel, history partials) timed with HIP
 events on the launch stream, against its algorithmic bytes (114 B per
 token-head); ``cpu_baseline`` times the CPU oracle on a bounded sample.
 """
@@ -108,7 +108,7 @@ def bench_decode(args, dev):
                    "value_group": 32, "storage_dtype": "bf16", "layout": "contiguous FlatCache"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "kernel": "attn_hist_kernel", "kernel_ms": kern_ms,
+                     "kernel": "decode_mfma_kernel", "kernel_ms": kern_ms,
                      "algorithmic_bytes": algo_bytes, "bytes_per_token_head": bytes_per_th},
         "cpu_baseline": cpu,
         "extra": {"encode_cache_s": encode_s, "encode_boundary_ties": ties,
@@ -139,6 +139,24 @@ def cpu_baseline_decode(strat, keys, vals, q, Hq, Hkv, D, bits):
                       f"median of 3 after 1 warm-up; {t * 1e3:.1f} ms per sequence-step"}
 
 
+def copy_ceiling(dev, nbytes: int = 1 << 30, reps: int = 10):
+    """Device-to-device copy of nbytes: the practical HBM ceiling (read +
+    write bytes / time) and the reference kernel for counter calibration."""
+    src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    a, b = _events(2)
+    a.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / reps
+    return {"copy_bytes": nbytes, "copy_ms": ms, "copy_gbs": 2 * nbytes / (ms * 1e-3) / 1e9}
+
+
 # --------------------------------------------------------------- main ---
 
 def main():
@@ -150,6 +168,8 @@ def main():
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--context", type=int, default=32768)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run a 1 GiB device copy (HBM ceiling and counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path "
@@ -160,6 +180,9 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
     dev = torch.device("cuda:0")
+    if args.copy_probe:
+        print(json.dumps(copy_ceiling(dev)), flush=True)
+        return
     res = bench_decode(args, dev)
     print(json.dumps(res), flush=True)
 

@@ -197,6 +197,10 @@ typedef struct smaq_attn_params {
      Phases communicate through the workspace, launched in order on one
      stream. */
   int phases;
+  /* kernel choice: 0 = automatic (matrix-core decode kernel when the shape
+     allows, generic kernels otherwise), 1 = generic kernels only, 2 = the
+     matrix-core decode kernel (SMAQ_EUNSUPPORTED if the shape does not fit). */
+  int impl;
 } smaq_attn_params;
 
 /* Bytes of workspace smaq_attn_hybrid needs for these parameters. */

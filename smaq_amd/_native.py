@@ -51,7 +51,7 @@ class AttnParams(ctypes.Structure):
         ("out", c_void_p), ("out_dtype", c_int),
         ("workspace", c_void_p), ("workspace_bytes", c_ll),
         ("max_hist_len", c_ll), ("max_recent_len", c_ll),
-        ("phases", c_int),
+        ("phases", c_int), ("impl", c_int),
     ]
 
 

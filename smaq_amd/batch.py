@@ -76,7 +76,8 @@ class QuantizedKVBatch:
         return n
 
     def plan(self, query: torch.Tensor, scale: Optional[float] = None, recent_k: Optional[torch.Tensor] = None,
-             recent_v: Optional[torch.Tensor] = None, recent_len: Optional[torch.Tensor] = None) -> AttentionPlan:
+             recent_v: Optional[torch.Tensor] = None, recent_len: Optional[torch.Tensor] = None,
+             impl: int = 0) -> AttentionPlan:
         """A reusable decode launch for queries shaped like ``query`` ([B, Hq, D]
         or [B, T, Hq, D]); see ``score.AttentionPlan``."""
         q = query.unsqueeze(1) if query.dim() == 3 else query
@@ -90,15 +91,16 @@ class QuantizedKVBatch:
             hist_len=None if self.uniform else self.hist_len, max_hist_len=max(self.seq_lens),
             hist_seq_start=None if self.uniform else self.seq_start, hist_head_stride=self.total,
             recent_k=recent_k, recent_v=recent_v, recent_len=recent_len, max_recent_len=max_r,
-            scale=scale, out_dtype=query.dtype, hist_pos_offset=0)
+            scale=scale, out_dtype=query.dtype, hist_pos_offset=0, impl=impl)
 
     def attention(self, query: torch.Tensor, scale: Optional[float] = None,
                   recent_k: Optional[torch.Tensor] = None, recent_v: Optional[torch.Tensor] = None,
-                  recent_len: Optional[torch.Tensor] = None) -> torch.Tensor:
+                  recent_len: Optional[torch.Tensor] = None, impl: int = 0) -> torch.Tensor:
         """query [B, Hq, D] (one decode token per sequence) or [B, T, Hq, D];
         recent_k/v [B, R, Hkv, D] with per-sequence recent_len.  Returns the
-        query's shape in its dtype."""
-        out = self.plan(query, scale, recent_k, recent_v, recent_len).run(query)
+        query's shape in its dtype.  ``impl``: 0 automatic, 1 generic kernels,
+        2 matrix-core decode kernel."""
+        out = self.plan(query, scale, recent_k, recent_v, recent_len, impl).run(query)
         return out.squeeze(1) if query.dim() == 3 else out
 
 
@@ -141,7 +143,7 @@ class PagedQuantizedKV:
         return cls(strategy, codes, norms, vd, vs, vz, block_table, [k.shape[0] for k in keys], block_size,
                    value_bits, value_group)
 
-    def plan(self, query: torch.Tensor, scale: Optional[float] = None) -> AttentionPlan:
+    def plan(self, query: torch.Tensor, scale: Optional[float] = None, impl: int = 0) -> AttentionPlan:
         q = query.unsqueeze(1)
         D = q.shape[-1]
         scale = 1.0 / math.sqrt(D) if scale is None else scale
@@ -150,15 +152,15 @@ class PagedQuantizedKV:
             val_data=self.v_data, val_scales=self.v_scales, val_zeros=self.v_zeros, val_bits=self.value_bits,
             val_group=self.value_group, n_kv_heads=self.num_kv_heads, hist_len=self.hist_len,
             max_hist_len=max(self.seq_lens), block_table=self.block_table, block_size=self.block_size,
-            scale=scale, out_dtype=query.dtype)
+            scale=scale, out_dtype=query.dtype, impl=impl)
 
     def nbytes_per_token_head(self) -> int:
         n = self.codes.shape[-1] + (self.norms.element_size() if self.norms is not None else 0)
         return n + self.v_data.shape[-1] + 2 * self.v_scales.shape[-1] * self.v_scales.element_size()
 
-    def attention(self, query: torch.Tensor, scale: Optional[float] = None) -> torch.Tensor:
+    def attention(self, query: torch.Tensor, scale: Optional[float] = None, impl: int = 0) -> torch.Tensor:
         """query [B, Hq, D] -> [B, Hq, D]."""
-        return self.plan(query, scale).run(query).squeeze(1)
+        return self.plan(query, scale, impl).run(query).squeeze(1)
 
 
 def require_native() -> None:

@@ -18,7 +18,7 @@
 // (q . k) * scale, all fp32.
 #include <math.h>
 
-#include "smaq_common.h"
+#include "attention_internal.h"
 
 namespace smaq {
 
@@ -26,35 +26,6 @@ constexpr int kAttnThreads = 256;
 constexpr int kChunk = 64;       // tokens per online-softmax step
 constexpr int kRowTile = 16;     // query rows per workgroup
 constexpr int kMaxHeadDim = 256;
-
-struct HistAddr {
-  const long long* seq_start;  // NULL: sequence b starts at b * uniform_len
-  long long uniform_len;
-  long long head_stride;
-  const int* table;
-  int max_blocks, block_size, n_kv;
-  __device__ __forceinline__ int64_t row(int b, int h, int64_t t) const {
-    if (table) {
-      const int blk = table[(int64_t)b * max_blocks + t / block_size];
-      return ((int64_t)blk * n_kv + h) * block_size + (t % block_size);
-    }
-    return (int64_t)h * head_stride + (seq_start ? seq_start[b] : (int64_t)b * uniform_len) + t;
-  }
-};
-
-struct Partials {
-  float* m;  // [B][Hkv][rows][S]
-  float* l;
-  float* o;  // [B][Hkv][rows][S][D]
-  int S;
-  __device__ __forceinline__ int64_t idx(int b, int h, int nkv, int rows, int r, int s) const {
-    return (((int64_t)b * nkv + h) * rows + r) * S + s;
-  }
-};
-
-struct Seg {
-  int64_t t0, t1;  // token range of this split inside the sequence
-};
 
 // Online softmax over one chunk of scores already in sc[r][0..kChunk).
 __device__ __forceinline__ void softmax_chunk(float (*sc)[kChunk], float* m_s, float* l_s,
@@ -383,6 +354,7 @@ struct Plan {
   int row_tiles;
   int64_t hist_split, recent_split;
   int s_hist, s_recent;
+  bool mfma;
 };
 
 static Plan make_plan(const smaq_attn_params* p) {
@@ -390,6 +362,7 @@ static Plan make_plan(const smaq_attn_params* p) {
   const int g = p->n_q_heads / p->n_kv_heads;
   const int rows = p->q_len * g;
   pl.row_tiles = (rows + kRowTile - 1) / kRowTile;
+  pl.mfma = p->impl != 1 && p->has_history && mfma_decode_supported(*p);
   const int64_t units = (int64_t)p->batch * p->n_kv_heads * pl.row_tiles;
   // aim for >= 2048 workgroups over the history
   int64_t want = units >= 2048 ? 1 : (2048 + units - 1) / units;
@@ -397,6 +370,7 @@ static Plan make_plan(const smaq_attn_params* p) {
   int64_t split = hl > 0 ? (hl + want - 1) / want : kChunk;
   split = ((split + kChunk - 1) / kChunk) * kChunk;
   if (split < 4 * kChunk) split = 4 * kChunk;
+  if (pl.mfma) split = mfma_decode_split_len(*p);
   pl.hist_split = split;
   pl.s_hist = hl > 0 ? (int)((hl + split - 1) / split) : 0;
   int64_t rl = p->has_recent ? p->max_recent_len : 0;
@@ -471,6 +445,10 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
                  "smaq_attn_hybrid: null recent pointer");
   }
   const Plan pl = make_plan(&p);
+  if (p.impl == 2 && !pl.mfma) {
+    set_error("smaq_attn_hybrid: the matrix-core decode kernel does not serve this shape");
+    return SMAQ_EUNSUPPORTED;
+  }
   const long long need = smaq_attn_workspace_bytes(&p);
   SMAQ_REQUIRE(p.workspace_bytes >= need, "smaq_attn_hybrid: workspace %lld < %lld bytes",
                p.workspace_bytes, need);
@@ -489,7 +467,10 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
     HistAddr a{p.hist_seq_start, p.max_hist_len, p.hist_head_stride, p.block_table, p.max_blocks,
                p.block_size, p.n_kv_heads};
     int rc = SMAQ_EUNSUPPORTED;
-    if (p.key_format == SMAQ_KEY_SCALAR) {
+    if (pl.mfma) {
+      rc = launch_mfma_decode(p, a, part, pl.hist_split, pl.s_hist, st);
+      if (rc != SMAQ_OK) return rc;
+    } else if (p.key_format == SMAQ_KEY_SCALAR) {
       switch (p.norm_dtype) {
         case SMAQ_F32: rc = dispatch_hist_v<SMAQ_KEY_SCALAR, float>(p, a, part, pl, st); break;
         case SMAQ_F16: rc = dispatch_hist_v<SMAQ_KEY_SCALAR, _Float16>(p, a, part, pl, st); break;
@@ -500,7 +481,7 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
       rc = dispatch_hist_v<SMAQ_KEY_BLOCKVQ, float>(p, a, part, pl, st);
     }
     if (rc != SMAQ_OK) return rc;
-    if ((rc = launch_status("smaq_attn_hybrid(history)")) != SMAQ_OK) return rc;
+    if (!pl.mfma && (rc = launch_status("smaq_attn_hybrid(history)")) != SMAQ_OK) return rc;
   }
   if (pl.s_recent > 0 && (phases & 2)) {
     dim3 grid(pl.s_recent, p.n_kv_heads * pl.row_tiles, p.batch);

@@ -1,0 +1,621 @@
+// Decode attention over scalar-coded keys on the gfx950 matrix cores.
+//
+// Serves the common decode shape: head_dim 128, 3- or 4-bit scalar key codes
+// (two per byte), 2-bit values in groups of 32, one query token per sequence
+// and up to 4 query heads per KV head.  One workgroup = 4 waves over one
+// (context split, KV head, sequence); each wave streams 32-token tiles, and
+// loads the next tile's rows while it computes the current one.
+//
+// Per 32-token tile (two 16-token halves):
+//   QK   v_mfma_f32_16x16x32_f16, M = 16 tokens, K = 32 dims, N = 16 columns:
+//        columns [0, Q) hold the query hi parts, [8, 8+Q) the lo parts.  The
+//        decoded key is split hi/lo as well (q.k ~= qh.kh + ql.kh + qh.kl), so
+//        scores keep ~22 bits against fp32.  Key bytes (two codes) go through
+//        a 256-entry LDS table that returns both codes' f16 hi and lo halves.
+//   soft the hi and lo columns are summed with one DPP add and the 4 x 32
+//        (query, token) scores are redistributed two per lane; online softmax
+//        in base 2 whose reference maximum is raised only when a score exceeds
+//        it by 2^8, so the cross-lane max and the rescale are rare.
+//   PV   v_mfma_f32_16x16x32_bf16, M = 16 rows (query head j, value group g),
+//        K = 32 tokens, N = 16 dims.  A = p * scale_g split bf16 hi/lo, staged
+//        through LDS in MFMA layout.  B: the value codes are spread to 16-bit
+//        lanes once per tile (LDS), and step tau takes bit field tau >> 1 of
+//        code byte 16*(tau & 1) + n as the bf16 value 128 + (c << 2f) with one
+//        and-or per dword; the 128 * sum(A) offset (an MFMA against ones), the
+//        2^2f column factor and the zero-point term sum(p * zero) are removed
+//        at the end.
+// Scores and outputs match the reference fp32 path to ~1e-6 relative; the
+// unsupported shapes use the generic kernels in attention.hip.
+#include <math.h>
+
+#include "attention_internal.h"
+
+namespace smaq {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kMWaves = 4;
+constexpr int kMTile = 32;
+constexpr int kVRow = 80;   // bytes per code-byte row of the spread value tile (64 + 16 pad)
+constexpr int kARow = 144;  // bytes per row of the staged PV A operand (64 hi + 64 lo + 16 pad)
+// The softmax reference maximum is raised only when a score exceeds it by
+// this much (log2 units), so weights stay below 2^8 and rescales are rare.
+constexpr float kLazyRescale = 8.0f;
+
+// Rows of one 32-token tile: tokens 0..15 at rows gA.., 16..31 at gB..
+struct TileDesc {
+  int64_t gA, gB;
+  int last;  // offsets [0, last] are valid tokens
+};
+
+__device__ __forceinline__ uint32_t f16_bits(_Float16 h) { return (uint32_t)__builtin_bit_cast(uint16_t, h); }
+
+__device__ __forceinline__ f16x8 as_f16x8(u32x4 v) { return __builtin_bit_cast(f16x8, v); }
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// exponent e with |x| in [2^e, 2^(e+1)); 0 for x == 0
+__device__ __forceinline__ int exponent_of(float x) {
+  if (!(x > 0.0f)) return 0;
+  int e;
+  frexpf(x, &e);
+  return e - 1;
+}
+
+// Orders this wave's LDS writes before its later LDS reads of other lanes'
+// data (a wave-local exchange; the workgroup's waves run independent tiles).
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// A wave-uniform 64-bit value, moved to SGPRs.
+__device__ __forceinline__ int64_t uniform64(int64_t x) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)x >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+// 2^x on the transcendental unit (v_exp_f32); denormal results flush to 0,
+// which is harmless for softmax weights.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Value of lane (i + 8) within each 16-lane row (row_shl:8); lanes 8..15 of a
+// row read 0.
+__device__ __forceinline__ float dpp_row_shl8(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x108, 0xf, 0xf, true));
+}
+
+// Lanes of the banks (4-lane groups of a 16-lane row) in BANKS take `src` from
+// the lane the DPP control CTRL names (row_shr:k = lane i - k); the others keep
+// `old`.
+template <int CTRL, int BANKS>
+__device__ __forceinline__ float dpp_bank_move(float old, float src) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old), __builtin_bit_cast(int, src),
+                                                               CTRL, 0xf, BANKS, false));
+}
+
+// Rotation within each 16-lane row (CTRL = row_ror:k); fuses into the
+// consuming max / add.
+template <int CTRL>
+__device__ __forceinline__ float dpp_row_ror(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xf, 0xf, true));
+}
+
+// (x & m) | c in one instruction (m in an SGPR, c in a VGPR).
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(m), "v"(c));
+  return r;
+}
+
+// Two consecutive storage-dtype values -> fp32 (one 4- or 8-byte load; the
+// element index must be even).
+template <typename T>
+__device__ __forceinline__ void load2(const T* p, float* out) {
+  if constexpr (sizeof(T) == 2) {
+    const uint32_t v = *(const uint32_t*)p;
+    out[0] = Num<T>::to_f(__builtin_bit_cast(T, (uint16_t)v));
+    out[1] = Num<T>::to_f(__builtin_bit_cast(T, (uint16_t)(v >> 16)));
+  } else {
+    const float2 v = *(const float2*)p;
+    out[0] = v.x; out[1] = v.y;
+  }
+}
+
+// Eight consecutive storage-dtype values, kept packed as loaded (16 or 32
+// bytes; the element index must be a multiple of 8) and widened on use.
+template <typename T>
+struct Pack8 {
+  static constexpr int kWords = sizeof(T) == 2 ? 4 : 8;
+  uint32_t w[kWords];
+  __device__ __forceinline__ void load(const T* p) {
+    if constexpr (sizeof(T) == 2) {
+      const uint4 v = *(const uint4*)p;
+      w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    } else {
+      const uint4 a = *(const uint4*)p, c = *(const uint4*)(p + 4);
+      w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+      w[4] = c.x; w[5] = c.y; w[6] = c.z; w[7] = c.w;
+    }
+  }
+  __device__ __forceinline__ void set(int i, T v) {  // element-wise fill
+    if constexpr (sizeof(T) == 2) {
+      const uint32_t bits = (uint32_t)__builtin_bit_cast(uint16_t, v);
+      w[i >> 1] = (i & 1) ? ((w[i >> 1] & 0xffffu) | (bits << 16)) : ((w[i >> 1] & 0xffff0000u) | bits);
+    } else {
+      w[i] = __builtin_bit_cast(uint32_t, v);
+    }
+  }
+  __device__ __forceinline__ float get(int i) const {
+    if constexpr (sizeof(T) == 2)
+      return Num<T>::to_f(__builtin_bit_cast(T, (uint16_t)(w[i >> 1] >> (16 * (i & 1)))));
+    else
+      return __builtin_bit_cast(float, w[i]);
+  }
+};
+
+template <int KBITS, typename TN, typename TV>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void decode_mfma_kernel(
+    smaq_attn_params p, HistAddr addr, Partials part, int64_t split_len) {
+  __shared__ uint32_t lut[2][256];  // [0]: f16 hi pair, [1]: f16 lo pair
+  // per wave: value codes spread to 16 bits ([code byte][token pair] dwords)
+  // and the PV A operand ([row][hi 32 tokens | lo 32 tokens] bf16)
+  __shared__ __attribute__((aligned(16))) uint8_t vsp[kMWaves][32 * kVRow];
+  __shared__ __attribute__((aligned(16))) uint8_t ast[kMWaves][16 * kARow];
+  __shared__ float red_m[kMWaves][4];
+  __shared__ float red_l[kMWaves][4];
+  __shared__ float red_o[kMWaves][4][128];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6;
+  const int wu = __builtin_amdgcn_readfirstlane(w);  // wave index, in an SGPR
+  const int n = lane & 15, kg = lane >> 4;           // MFMA lane coordinates
+  const int bank = n >> 2, qq = n & 3;               // softmax layout: bank, query row
+  // this lane's two softmax tokens: C-layout values 2*bank, 2*bank + 1
+  const int tokA = bank < 2 ? 4 * kg + 2 * bank : 16 + 4 * kg + 2 * (bank - 2);
+  const int tq = lane & 7, pq = lane >> 3;           // value loader: tokens 4tq.., bytes 4pq..
+  const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int Q = p.n_q_heads / p.n_kv_heads;  // query rows (decode: one token)
+  constexpr uint32_t kMask = (1u << KBITS) - 1u;
+  constexpr float kLog2e = 1.4426950408889634f;
+
+  // ---- key LUT: byte (c0 | c1 << KBITS) -> packed f16 hi / lo of both codes,
+  // centroids pre-scaled by 2^-e_lut so the largest has magnitude in [1, 2)
+  float cmax = 0.0f;
+  for (int i = 0; i < (1 << KBITS); ++i) cmax = fmaxf(cmax, fabsf(p.key_lut[i]));
+  const int e_lut = exponent_of(cmax);
+  const float lut_scale = ldexpf(1.0f, -e_lut);
+  for (int v = tid; v < 256; v += 256) {
+    const float c0 = p.key_lut[v & kMask] * lut_scale;
+    const float c1 = p.key_lut[(v >> KBITS) & kMask] * lut_scale;
+    const _Float16 h0 = (_Float16)c0, h1 = (_Float16)c1;
+    const _Float16 l0 = (_Float16)(c0 - (float)h0), l1 = (_Float16)(c1 - (float)h1);
+    lut[0][v] = f16_bits(h0) | (f16_bits(h1) << 16);
+    lut[1][v] = f16_bits(l0) | (f16_bits(l1) << 16);
+  }
+
+  // ---- query B operands: columns [0, Q) hold the hi parts of query rows
+  // 0..Q-1, columns [8, 8+Q) their lo parts, the rest zero
+  const int qrow = n < Q ? n : ((n >= 8 && n < 8 + Q) ? n - 8 : -1);
+  const float* qsrc = p.q_hist + ((int64_t)b * p.n_q_heads + h * Q + (qrow < 0 ? 0 : qrow)) * 128;
+  float qv[32];
+  float qmax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    qv[i] = qrow < 0 ? 0.0f : qsrc[32 * kg + i];
+    qmax = fmaxf(qmax, fabsf(qv[i]));
+  }
+  qmax = fmaxf(qmax, __shfl_xor(qmax, 16, 64));
+  qmax = fmaxf(qmax, __shfl_xor(qmax, 32, 64));
+  const int e_q = exponent_of(qmax);
+  const float q_scale = ldexpf(1.0f, -e_q);
+  // Step st (0..7) covers dims d = 32kg + 4st + {0..3}; its 8 k-elements are
+  // [x(d0) x(d1) y(d0) y(d1) x(d2) x(d3) y(d2) y(d3)], matched on the key side by
+  // [hi(d0) hi(d1) lo(d0) lo(d1) hi(d2) hi(d3) lo(d2) lo(d3)] (two LUT pairs).
+  // x = q hi (columns < Q) or q lo (columns 8..8+Q), y = q hi (columns < Q), so
+  // column j + column 8+j = qh.kh + qh.kl + ql.kh.
+  u32x4 bq[8];
+#pragma unroll
+  for (int st = 0; st < 8; ++st) {
+    uint32_t xw[2], yw[2];
+#pragma unroll
+    for (int pr2 = 0; pr2 < 2; ++pr2) {
+      uint32_t xx = 0, yy = 0;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const float x = qv[4 * st + 2 * pr2 + hh] * q_scale;
+        const _Float16 hi = (_Float16)x;
+        const _Float16 lo = (_Float16)(x - (float)hi);
+        const uint32_t hb = f16_bits(hi), lb = f16_bits(lo);
+        xx |= (n < Q ? hb : (qrow >= 0 ? lb : 0u)) << (16 * hh);
+        yy |= (n < Q ? hb : 0u) << (16 * hh);
+      }
+      xw[pr2] = xx;
+      yw[pr2] = yy;
+    }
+    bq[st] = u32x4{xw[0], yw[0], xw[1], yw[1]};
+  }
+  // score factor of query row qq: scale * log2(e) * 2^(e_q + e_lut), taken
+  // from column qq (its hi column)
+  const float rfac = __shfl(p.scale * kLog2e * ldexpf(1.0f, e_q + e_lut), qq, 64);
+  __syncthreads();
+
+  // ---- split range
+  // (wave-uniform values are pinned to SGPRs so the tile loop's control flow
+  // and address arithmetic stay scalar)
+  const int64_t len = uniform64(p.hist_len ? min((int64_t)p.hist_len[b], (int64_t)p.max_hist_len) : p.max_hist_len);
+  const int64_t s0 = (int64_t)s * split_len;
+  const int64_t s1 = uniform64(min(len, s0 + split_len));
+  const uint8_t* kbytes = (const uint8_t*)p.key_bytes;
+  const uint8_t* vbytes = (const uint8_t*)p.val_bytes;
+  const TN* norms = (const TN*)p.key_norms;
+  const TV* vsc = (const TV*)p.val_scales;
+  const TV* vzr = (const TV*)p.val_zeros;
+
+  // reference max / running sum of query row qq (max replicated over its 16
+  // lanes; the sum is this lane's share, reduced once at the end)
+  float m_run = -__builtin_inff(), l_run = 0.0f;
+  f32x4 acc_o[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc_o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 acc_s = {0.f, 0.f, 0.f, 0.f};  // sum of A per row (query kg, group v)
+  float zacc[4] = {0.f, 0.f, 0.f, 0.f};  // this lane's share of sum p * zero, query qq
+  const u32x4 kOnesBf16 = u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+  const uint32_t kBf16Base = 0x43004300u;  // bf16 128.0 in both halves
+
+  // LDS addresses (lane constants)
+  uint8_t* const vw = &vsp[w][kVRow * 4 * pq + 8 * tq];       // spread writer, code byte 4pq
+  const uint8_t* const vr = &vsp[w][kVRow * n + 16 * kg];     // B reader: byte n (+16 rows: 16+n)
+  uint8_t* const aw = &ast[w][kARow * 4 * qq + 4 * (tokA >> 1)];  // A writer: row (qq, group 0)
+  const uint8_t* const ar = &ast[w][kARow * n + 16 * kg];     // A reader: row n, tokens 8kg..
+
+  // row of history token t0g (a multiple of 16): rows t0g .. t0g + 15 are
+  // consecutive in both layouts (paged blocks hold a multiple of 16 tokens)
+  const int64_t contig_base = uniform64(addr.table ? 0
+      : (int64_t)h * addr.head_stride + (addr.seq_start ? addr.seq_start[b] : (int64_t)b * addr.uniform_len));
+  // block table row of this sequence, read through the scalar cache
+  typedef const __attribute__((address_space(4))) int* ConstIntPtr;
+  const bool paged = __builtin_amdgcn_readfirstlane(addr.table != nullptr ? 1 : 0) != 0;
+  const ConstIntPtr tbl =
+      (ConstIntPtr)uniform64(paged ? (int64_t)(uintptr_t)(addr.table + (int64_t)b * addr.max_blocks) : 0);
+  const int bsz = addr.block_size;          // a power of two (checked on the host)
+  const int n_kv = addr.n_kv;
+  const int bshift = __builtin_ctz((unsigned)bsz);
+  auto group_row = [&](int64_t t0g) -> int64_t {
+    if (!paged) return contig_base + t0g;
+    const uint32_t tg = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)t0g);
+    const uint32_t blk_i = tg >> bshift;
+    const int blk = __builtin_amdgcn_readfirstlane(tbl[blk_i]);
+    return ((int64_t)blk * n_kv + h) * bsz + (tg & (uint32_t)(bsz - 1));
+  };
+
+  // Tile t (first token; a multiple of 32 past the split start): its rows and
+  // validity.  Offsets [0, last] are valid tokens; a tail tile clamps rows onto
+  // the last valid token.
+  auto describe = [&](int64_t t) -> TileDesc {
+    TileDesc d;
+    d.last = __builtin_amdgcn_readfirstlane((int)min((int64_t)31, s1 - 1 - t));
+    d.gA = uniform64(group_row(t));
+    d.gB = uniform64(d.last >= 16 ? group_row(t + 16) : d.gA);
+    return d;
+  };
+  auto rowof = [&](const TileDesc& d, int i) -> int64_t {
+    const int c = min(i, d.last);
+    return c < 16 ? d.gA + c : d.gB + (c - 16);
+  };
+  // this lane's first softmax token row (tokens tokA, tokA + 1 are consecutive rows)
+  auto rowA = [&](const TileDesc& d) -> int64_t { return tokA < 16 ? d.gA + tokA : d.gB + (tokA - 16); };
+
+  // Full tiles with even rows: vector loads, the same instructions for every
+  // tile (so the pipelined loop below waits on exact load counts).
+  auto fast_values = [&](const TileDesc& d, uint32_t* vd) {
+    const uint8_t* vrow = vbytes + ((tq < 4 ? d.gA : d.gB) + 4 * (tq & 3)) * 32 + 4 * pq;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) vd[i] = *(const uint32_t*)(vrow + 32 * i);
+  };
+  auto fast_keys = [&](const TileDesc& d, u32x4& kqa, u32x4& kqb) {
+    const uint32_t off = (uint32_t)(n * 64 + 16 * kg);
+    kqa = *(const u32x4*)(kbytes + d.gA * 64 + off);
+    kqb = *(const u32x4*)(kbytes + d.gB * 64 + off);
+  };
+  auto fast_norms = [&](const TileDesc& d, float* nrm) { load2<TN>(norms + rowA(d), nrm); };
+  auto fast_side = [&](const TileDesc& d, Pack8<TV>& sv, Pack8<TV>& zv) {
+    const int64_t r = rowA(d);
+    sv.load(vsc + r * 4);
+    zv.load(vzr + r * 4);
+  };
+  // Any tile (tail or odd rows): element loads with clamped rows.
+  auto slow_loads = [&](const TileDesc& d, u32x4& kqa, u32x4& kqb, uint32_t* vd, float* nrm,
+                        Pack8<TV>& sv, Pack8<TV>& zv) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) vd[i] = *(const uint32_t*)(vbytes + rowof(d, 4 * tq + i) * 32 + 4 * pq);
+    kqa = *(const u32x4*)(kbytes + rowof(d, n) * 64 + 16 * kg);
+    kqb = *(const u32x4*)(kbytes + rowof(d, 16 + n) * 64 + 16 * kg);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int64_t r = rowof(d, tokA + i);
+      nrm[i] = Num<TN>::to_f(norms[r]);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        sv.set(4 * i + g, vsc[r * 4 + g]);
+        zv.set(4 * i + g, vzr[r * 4 + g]);
+      }
+    }
+  };
+
+  float m_thr = -__builtin_inff();  // m_run + kLazyRescale
+  // One tile.  The hooks run right after the tile's copy of the matching
+  // registers has been consumed (the pipelined loop loads the next tile there).
+  auto tile = [&](const TileDesc& dcur, u32x4& kqa, u32x4& kqb, uint32_t* vd, float* nrm,
+                  Pack8<TV>& sv, Pack8<TV>& zv, auto&& after_values, auto&& after_keys,
+                  auto&& after_norms, auto&& after_side) {
+    const int last = dcur.last;
+    const bool tail = last < 31;
+    // -- value codes spread to 16 bits: dword (byte j, tokens 2i, 2i+1) =
+    // [code byte of token 2i, 0, code byte of token 2i+1, 0]
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t sel = 0x0c000c00u | ((uint32_t)(4 + j) << 16) | (uint32_t)j;
+      uint2 pr2;
+      pr2.x = __builtin_amdgcn_perm(vd[1], vd[0], sel);
+      pr2.y = __builtin_amdgcn_perm(vd[3], vd[2], sel);
+      *(uint2*)(vw + kVRow * j) = pr2;
+    }
+    after_values();
+    // -- QK: per step two key bytes -> two LUT pairs -> one A operand
+    f32x4 ca = {0.f, 0.f, 0.f, 0.f}, cb = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+      const uint32_t wa = kqa[st >> 1] >> (16 * (st & 1)), wb = kqb[st >> 1] >> (16 * (st & 1));
+      const uint32_t a0 = wa & 0xffu, a1 = (wa >> 8) & 0xffu;
+      const uint32_t b0 = wb & 0xffu, b1 = (wb >> 8) & 0xffu;
+      const u32x4 av = u32x4{lut[0][a0], lut[1][a0], lut[0][a1], lut[1][a1]};
+      const u32x4 bv = u32x4{lut[0][b0], lut[1][b0], lut[0][b1], lut[1][b1]};
+      ca = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(av), as_f16x8(bq[st]), ca, 0, 0, 0);
+      cb = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(bv), as_f16x8(bq[st]), cb, 0, 0, 0);
+    }
+    after_keys();
+    // -- scores.  C layout: lane (kg, n) holds column n for tokens 4kg + v (ca)
+    // and 16 + 4kg + v (cb).  Add the lo column n + 8 (row_shl:8), then move
+    // values 2*bank, 2*bank + 1 of column qq into bank `bank` of the same row.
+    float sc[8];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      sc[v] = ca[v] + dpp_row_shl8(ca[v]);
+      sc[4 + v] = cb[v] + dpp_row_shl8(cb[v]);
+    }
+    float x0 = sc[0], x1 = sc[1];
+    x0 = dpp_bank_move<0x114, 0x2>(x0, sc[2]);  // row_shr:4 into bank 1
+    x1 = dpp_bank_move<0x114, 0x2>(x1, sc[3]);
+    x0 = dpp_bank_move<0x118, 0x4>(x0, sc[4]);  // row_shr:8 into bank 2
+    x1 = dpp_bank_move<0x118, 0x4>(x1, sc[5]);
+    x0 = dpp_bank_move<0x11c, 0x8>(x0, sc[6]);  // row_shr:12 into bank 3
+    x1 = dpp_bank_move<0x11c, 0x8>(x1, sc[7]);
+    x0 *= nrm[0];  // score / rfac (rfac > 0 is applied in the exponent)
+    x1 *= nrm[1];
+    after_norms();
+    if (tail) {
+      if (tokA > last) x0 = -__builtin_inff();
+      if (tokA + 1 > last) x1 = -__builtin_inff();
+    }
+    // -- online softmax (base 2) of query row qq over its 16 lanes, with a
+    // lazily raised reference maximum: weights may grow to 2^kLazyRescale
+    // before the row maximum is reduced and the accumulators rescaled.
+    const float tmax = fmaxf(x0, x1) * rfac;
+    if (__any(tmax > m_thr)) {
+      float mt = tmax;
+      mt = fmaxf(mt, dpp_row_ror<0x124>(mt));
+      mt = fmaxf(mt, dpp_row_ror<0x128>(mt));
+      mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+      const float m_new = fmaxf(m_run, mt);
+      // rows qq >= Q are padding: their factor stays 1
+      const float alpha = qq >= Q ? 1.0f : ((m_run == -__builtin_inff()) ? 0.0f : fast_exp2(m_run - m_new));
+      const float a_o = __shfl(alpha, kg, 64);  // O rows: query kg (lane kg holds row kg)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc_o[i] *= a_o;
+      acc_s *= a_o;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) zacc[g] *= alpha;
+      l_run *= alpha;
+      m_run = m_new;
+      m_thr = m_new + kLazyRescale;
+    }
+    // exp2(-inf) = 0 covers masked tokens; only a row with no valid token yet
+    // (m_run = -inf, possible in a tail tile) needs the guard against inf - inf
+    const bool dead = tail && m_run == -__builtin_inff();
+    const float p0 = dead ? 0.0f : fast_exp2(fmaf(x0, rfac, -m_run));
+    const float p1 = dead ? 0.0f : fast_exp2(fmaf(x1, rfac, -m_run));
+    l_run += p0 + p1;
+    // -- PV A operand (row (qq, g), tokens tokA, tokA + 1): p * scale split into
+    // a bf16 hi part (truncation, exact remainder) and a rounded bf16 lo part
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float ps0 = p0 * sv.get(g), ps1 = p1 * sv.get(4 + g);
+      const uint32_t h0 = __builtin_bit_cast(uint32_t, ps0) & 0xffff0000u;
+      const uint32_t h1 = __builtin_bit_cast(uint32_t, ps1) & 0xffff0000u;
+      const f32x2 lo2 = {ps0 - __builtin_bit_cast(float, h0), ps1 - __builtin_bit_cast(float, h1)};
+      const uint32_t hp = __builtin_amdgcn_perm(h1, h0, 0x07060302u);
+      const uint32_t lp = __builtin_bit_cast(uint32_t, __builtin_convertvector(lo2, bf16x2));
+      *(uint32_t*)(aw + kARow * g) = hp;
+      *(uint32_t*)(aw + kARow * g + 64) = lp;
+      zacc[g] = fmaf(p1, zv.get(4 + g), fmaf(p0, zv.get(g), zacc[g]));
+    }
+    after_side();
+    wave_sync();
+    // -- PV.  A: rows (query kg', group g') x tokens 8kg..8kg+7.  B: column n of
+    // step tau is code byte 16*(tau & 1) + n, bit field f = tau >> 1 (dim
+    // 4 * byte + f), as the bf16 value 128 + (c << 2f) (f = 3: 128 + 32c), so
+    // each step is one and-or per dword.
+    const u32x4 ahi = *(const u32x4*)(ar);
+    const u32x4 alo = *(const u32x4*)(ar + 64);
+    const u32x4 w0 = *(const u32x4*)(vr);
+    const u32x4 w1 = *(const u32x4*)(vr + kVRow * 16);
+    acc_s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ahi), as_bf16x8(kOnesBf16), acc_s, 0, 0, 0);
+    acc_s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(alo), as_bf16x8(kOnesBf16), acc_s, 0, 0, 0);
+#pragma unroll
+    for (int tau = 0; tau < 8; ++tau) {
+      const u32x4 wv = (tau & 1) ? w1 : w0;
+      const int f = tau >> 1;
+      u32x4 bv;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        bv[i] = f < 3 ? and_or(wv[i], 0x00030003u << (2 * f), kBf16Base)
+                      : and_or(wv[i] >> 1, 0x00600060u, kBf16Base);
+      acc_o[tau] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ahi), as_bf16x8(bv), acc_o[tau], 0, 0, 0);
+      acc_o[tau] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(alo), as_bf16x8(bv), acc_o[tau], 0, 0, 0);
+    }
+    wave_sync();  // this tile's LDS reads complete before the next tile's writes
+  };
+
+  u32x4 kqa, kqb;
+  uint32_t vd[4];
+  float nrm[2];
+  Pack8<TV> sv, zv;
+  auto none = [] {};
+  int64_t t0 = s0 + (int64_t)wu * kMTile;
+  // Pipelined loop over full tiles with even rows (paged rows always are;
+  // contiguous rows when the head's first row is even).  Each iteration
+  // issues the next tile's loads as soon as this tile's registers are free,
+  // so every load has one iteration to arrive; the last iteration reloads its
+  // own rows (cache hits) to keep the load sequence identical.
+  const bool even_rows = paged || (contig_base & 1) == 0;
+  if (even_rows && t0 + kMTile <= s1) {
+    TileDesc dc = describe(t0);
+    fast_values(dc, vd);
+    fast_keys(dc, kqa, kqb);
+    fast_norms(dc, nrm);
+    fast_side(dc, sv, zv);
+    for (;;) {
+      t0 = uniform64(t0);
+      const int64_t tn = t0 + kMWaves * kMTile;
+      const bool more = __builtin_amdgcn_readfirstlane((int)(tn + kMTile <= s1)) != 0;
+      const TileDesc dn = more ? describe(tn) : dc;
+      tile(dc, kqa, kqb, vd, nrm, sv, zv,
+           [&] { fast_values(dn, vd); }, [&] { fast_keys(dn, kqa, kqb); },
+           [&] { fast_norms(dn, nrm); }, [&] { fast_side(dn, sv, zv); });
+      t0 = tn;
+      dc = dn;
+      if (!more) break;
+    }
+  }
+  // Remaining tiles (the tail, or rows of odd parity): loads at the top.
+  for (; t0 < s1; t0 += kMWaves * kMTile) {
+    t0 = uniform64(t0);
+    const TileDesc d = describe(t0);
+    slow_loads(d, kqa, kqb, vd, nrm, sv, zv);
+    tile(d, kqa, kqb, vd, nrm, sv, zv, none, none, none, none);
+  }
+
+  // ---- per-wave result.  Sum the per-lane shares of query qq (banks, rows).
+  l_run += dpp_row_ror<0x124>(l_run);
+  l_run += dpp_row_ror<0x128>(l_run);
+  l_run += __shfl_xor(l_run, 16, 64);
+  l_run += __shfl_xor(l_run, 32, 64);
+  float zq[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    float z = zacc[g];
+    z += dpp_row_ror<0x124>(z);
+    z += dpp_row_ror<0x128>(z);
+    z += __shfl_xor(z, 16, 64);
+    z += __shfl_xor(z, 32, 64);
+    zq[g] = __shfl(z, kg, 64);  // query kg
+  }
+  if (kg < Q) {
+    // C element (row (kg, g), column n) of step tau: dim 4 * (16 * (tau & 1) + n) + (tau >> 1),
+    // which lies in group g = 2 * (tau & 1) + (n >> 3)
+#pragma unroll
+    for (int tau = 0; tau < 8; ++tau) {
+      const int hb = tau & 1, f = tau >> 1;
+      const bool hi8 = n >= 8;
+      const float acc = hi8 ? acc_o[tau][2 * hb + 1] : acc_o[tau][2 * hb];
+      const float sg = hi8 ? acc_s[2 * hb + 1] : acc_s[2 * hb];
+      const float zg = hi8 ? zq[2 * hb + 1] : zq[2 * hb];
+      const float inv = f < 3 ? 1.0f / (float)(1 << (2 * f)) : 1.0f / 32.0f;
+      red_o[w][kg][4 * (16 * hb + n) + f] = (acc - 128.0f * sg) * inv + zg;
+    }
+  }
+  if (lane < Q) {
+    red_m[w][lane] = m_run;
+    red_l[w][lane] = l_run;
+  }
+  __syncthreads();
+  // ---- merge the 4 waves into this split's partial (natural-log units)
+  for (int i = tid; i < Q * 128; i += 256) {
+    const int j = i >> 7, d = i & 127;
+    float M = -__builtin_inff();
+    for (int ww = 0; ww < kMWaves; ++ww)
+      if (red_l[ww][j] > 0.0f) M = fmaxf(M, red_m[ww][j]);
+    float L = 0.0f, O = 0.0f;
+    for (int ww = 0; ww < kMWaves; ++ww) {
+      if (!(red_l[ww][j] > 0.0f)) continue;
+      const float f = exp2f(red_m[ww][j] - M);
+      L = fmaf(red_l[ww][j], f, L);
+      O = fmaf(red_o[ww][j][d], f, O);
+    }
+    const int64_t pi = part.idx(b, h, p.n_kv_heads, Q, j, s);
+    part.o[pi * 128 + d] = O;
+    if (d == 0) {
+      part.m[pi] = M == -__builtin_inff() ? M : M * 0.6931471805599453f;
+      part.l[pi] = L;
+    }
+  }
+}
+
+bool mfma_decode_supported(const smaq_attn_params& p) {
+  const int g = p.n_q_heads / p.n_kv_heads;
+  return p.has_history && p.q_len == 1 && !p.q_positions && p.head_dim == 128 &&
+         p.key_format == SMAQ_KEY_SCALAR && (p.key_bits == 3 || p.key_bits == 4) &&
+         p.key_row_bytes == 64 && p.val_bits == 2 && p.val_group == 32 && p.val_row_bytes == 32 &&
+         g >= 1 && g <= 4 &&
+         (!p.block_table || (p.block_size >= 16 && (p.block_size & (p.block_size - 1)) == 0)) &&
+         // vector loads of rows and row pairs assume 16-byte aligned arrays
+         (((uintptr_t)p.key_bytes | (uintptr_t)p.val_bytes | (uintptr_t)p.key_norms |
+           (uintptr_t)p.val_scales | (uintptr_t)p.val_zeros) & 15) == 0;
+}
+
+int64_t mfma_decode_split_len(const smaq_attn_params& p) {
+  const int64_t units = (int64_t)p.batch * p.n_kv_heads;
+  const int64_t want = units >= 2048 ? 1 : (2048 + units - 1) / units;
+  int64_t split = (p.max_hist_len + want - 1) / want;
+  const int64_t q = kMWaves * kMTile;
+  split = ((split + q - 1) / q) * q;
+  return split < 4 * q ? 4 * q : split;
+}
+
+template <int KB, typename TN>
+static void launch_v(const smaq_attn_params& p, const HistAddr& a, const Partials& part,
+                     int64_t split_len, int n_splits, hipStream_t st) {
+  dim3 grid(n_splits, p.n_kv_heads, p.batch);
+  switch (p.val_dtype) {
+    case SMAQ_F32: hipLaunchKernelGGL((decode_mfma_kernel<KB, TN, float>), grid, dim3(256), 0, st, p, a, part, split_len); break;
+    case SMAQ_F16: hipLaunchKernelGGL((decode_mfma_kernel<KB, TN, _Float16>), grid, dim3(256), 0, st, p, a, part, split_len); break;
+    default: hipLaunchKernelGGL((decode_mfma_kernel<KB, TN, bf16>), grid, dim3(256), 0, st, p, a, part, split_len); break;
+  }
+}
+
+template <int KB>
+static void launch_n(const smaq_attn_params& p, const HistAddr& a, const Partials& part,
+                     int64_t split_len, int n_splits, hipStream_t st) {
+  switch (p.norm_dtype) {
+    case SMAQ_F32: launch_v<KB, float>(p, a, part, split_len, n_splits, st); break;
+    case SMAQ_F16: launch_v<KB, _Float16>(p, a, part, split_len, n_splits, st); break;
+    default: launch_v<KB, bf16>(p, a, part, split_len, n_splits, st); break;
+  }
+}
+
+int launch_mfma_decode(const smaq_attn_params& p, const HistAddr& a, const Partials& part,
+                       int64_t split_len, int n_splits, hipStream_t st) {
+  if (p.key_bits == 3) launch_n<3>(p, a, part, split_len, n_splits, st);
+  else launch_n<4>(p, a, part, split_len, n_splits, st);
+  return launch_status("smaq_attn_hybrid(mfma decode)");
+}
+
+}  // namespace smaq

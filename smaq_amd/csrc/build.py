@@ -37,6 +37,14 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-source extra flags.  The matrix-core decode kernel reduces maxima with
+# DPP; without IEEE mode (and with NaN-free arithmetic assumed) each step is one
+# fused v_max_f32_dpp instead of a DPP move plus two NaN-quieting maxima.
+EXTRA_FLAGS = {
+    "attention_mfma.hip": ["-fno-honor-nans", "-mno-amdgpu-ieee"],
+}
+
+
 def _hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and Path(cand).exists():
@@ -45,7 +53,7 @@ def _hipcc() -> str:
 
 
 def _compile(src: Path, obj: Path) -> None:
-    cmd = [_hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [_hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}\n{res.stderr}")

@@ -66,6 +66,7 @@ class AttentionPlan:
         query_positions: Optional[torch.Tensor] = None,
         hist_pos_offset: int = 0,
         recent_pos_offset: int = 0,
+        impl: int = 0,
     ):
         dev = _native.require_gpu(query, key_codes, val_data, recent_k)
         self.device = dev
@@ -77,6 +78,7 @@ class AttentionPlan:
         p = _native.AttnParams()
         p.batch, p.q_len, p.n_q_heads, p.n_kv_heads, p.head_dim = B, T, Hq, n_kv_heads, D
         p.scale = float(scale)
+        p.impl = int(impl)   # 0 auto, 1 generic kernels, 2 matrix-core decode kernel
         keep = []
         self.q_exact = torch.empty(B, T, Hq, D, dtype=torch.float32, device=dev)
         p.q_exact = self.q_exact.data_ptr()

@@ -70,22 +70,28 @@ def bench_decode(args, dev):
     for _ in range(args.warmup):
         plan.run(q)
     torch.cuda.synchronize()
-    ea, eb = _events(args.steps), _events(args.steps)
+    # timed region: K whole decode steps (query load + rotate, history
+    # partials, split combine), no events inside
     start, end = _events(2)
-    torch.cuda.synchronize()
     start.record()
+    for _ in range(args.steps):
+        plan.run(q)
+    end.record()
+    torch.cuda.synchronize()
+    ms_step = start.elapsed_time(end) / args.steps
+    # dominant kernel: HIP events on its launch stream (torch's current
+    # stream, which the plan launches on) around the history phase alone
+    ea, eb = _events(args.steps), _events(args.steps)
     for i in range(args.steps):
         plan.load_query(q)
         ea[i].record()
-        plan.launch(phases=1)          # history partials: the dominant kernel
+        plan.launch(phases=1)
         eb[i].record()
-        plan.launch(phases=4)          # split combine
-    end.record()
+        plan.launch(phases=4)
     torch.cuda.synchronize()
-    total_ms = start.elapsed_time(end)
-    ms_step = total_ms / args.steps
     kern_ms = statistics.mean(a.elapsed_time(b) for a, b in zip(ea, eb))
     achieved = algo_bytes / (kern_ms * 1e-3) / 1e9
+    traffic = recorded_traffic("decode_mfma_c3", dict(batch=B, context=N))
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -107,7 +113,7 @@ def bench_decode(args, dev):
                    "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "key_bits": bits, "value_bits": 2,
                    "value_group": 32, "storage_dtype": "bf16", "layout": "contiguous FlatCache"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
                      "kernel": "decode_mfma_kernel", "kernel_ms": kern_ms,
                      "algorithmic_bytes": algo_bytes, "bytes_per_token_head": bytes_per_th},
         "cpu_baseline": cpu,
@@ -139,6 +145,25 @@ def cpu_baseline_decode(strat, keys, vals, q, Hq, Hkv, D, bits):
                       f"median of 3 after 1 warm-up; {t * 1e3:.1f} ms per sequence-step"}
 
 
+def recorded_traffic(name: str, config: dict):
+    """HBM bytes per launch of the dominant kernel, as measured by the
+    rocprofv3 FETCH_SIZE / WRITE_SIZE passes recorded in profiles/<name>.md
+    (line ``traffic_bytes_per_launch = N``, with the config it was taken on).
+    None when no record matches this configuration."""
+    path = os.path.join(ROOT, "profiles", name + ".md")
+    if not os.path.exists(path):
+        return None
+    rec = {}
+    with open(path) as f:
+        for line in f:
+            if "=" in line and line.strip().startswith(("traffic_bytes_per_launch", "batch", "context")):
+                k, v = line.split("=", 1)
+                rec[k.strip()] = int(v.strip())
+    if "traffic_bytes_per_launch" not in rec or any(rec.get(k) != v for k, v in config.items()):
+        return None
+    return rec["traffic_bytes_per_launch"]
+
+
 def copy_ceiling(dev, nbytes: int = 1 << 30, reps: int = 10):
     """Device-to-device copy of nbytes: the practical HBM ceiling (read +
     write bytes / time) and the reference kernel for counter calibration."""
@@ -154,7 +179,19 @@ def copy_ceiling(dev, nbytes: int = 1 << 30, reps: int = 10):
     b.record()
     torch.cuda.synchronize()
     ms = a.elapsed_time(b) / reps
-    return {"copy_bytes": nbytes, "copy_ms": ms, "copy_gbs": 2 * nbytes / (ms * 1e-3) / 1e9}
+    # read-only ceiling: a full reduction over the same bytes as fp32
+    xf = src.view(torch.float32)
+    for _ in range(2):
+        xf.sum()
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(reps):
+        xf.sum()
+    b.record()
+    torch.cuda.synchronize()
+    rms = a.elapsed_time(b) / reps
+    return {"copy_bytes": nbytes, "copy_ms": ms, "copy_gbs": 2 * nbytes / (ms * 1e-3) / 1e9,
+            "read_ms": rms, "read_gbs": nbytes / (rms * 1e-3) / 1e9}
 
 
 # --------------------------------------------------------------- main ---

@@ -141,19 +141,35 @@ __global__ __launch_bounds__(kEncThreads) void encode_scalar_kernel(
 }
 
 // y[r][j] = (sum_d x[r][d] * Mt[d][j]) [* s[j]], sequential FMA over d.
+// out[r][j] = (sum_d x[r][d] * Mt[d][j]) [* s[j]], one sequential fmaf chain
+// over d per output (the reference's CPU matmul order).  A block holds
+// kRotRows rows in LDS and one thread per column j; each Mt element loaded
+// feeds kRotRows independent chains.
+constexpr int kRotRows = 8;
+
 template <typename T>
-__global__ __launch_bounds__(256) void rotate_rows_kernel(const T* __restrict__ x, int64_t rows,
-                                                          int D, const float* __restrict__ Mt,
-                                                          const float* __restrict__ s,
-                                                          float* __restrict__ out) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= rows * D) return;
-  const int64_t r = idx / D;
-  const int j = (int)(idx - r * D);
-  const T* xr = x + r * D;
-  float acc = 0.0f;
-  for (int d = 0; d < D; ++d) acc = fmaf(Num<T>::to_f(xr[d]), Mt[(int64_t)d * D + j], acc);
-  out[idx] = s ? acc * s[j] : acc;
+__global__ __launch_bounds__(1024) void rotate_rows_kernel(const T* __restrict__ x, int64_t rows,
+                                                           int D, const float* __restrict__ Mt,
+                                                           const float* __restrict__ s,
+                                                           float* __restrict__ out) {
+  extern __shared__ float xs[];  // [kRotRows][D]
+  const int j = threadIdx.x;
+  const int64_t r0 = (int64_t)blockIdx.x * kRotRows;
+  const int nr = (int)min((int64_t)kRotRows, rows - r0);
+  for (int i = 0; i < kRotRows; ++i)
+    xs[i * D + j] = i < nr ? Num<T>::to_f(x[(r0 + i) * D + j]) : 0.0f;
+  __syncthreads();
+  float acc[kRotRows];
+#pragma unroll
+  for (int i = 0; i < kRotRows; ++i) acc[i] = 0.0f;
+#pragma unroll 4
+  for (int d = 0; d < D; ++d) {
+    const float m = Mt[(int64_t)d * D + j];
+#pragma unroll
+    for (int i = 0; i < kRotRows; ++i) acc[i] = fmaf(xs[i * D + d], m, acc[i]);
+  }
+  const float sj = s ? s[j] : 1.0f;
+  for (int i = 0; i < nr; ++i) out[(r0 + i) * D + j] = s ? acc[i] * sj : acc[i];
 }
 
 __device__ __forceinline__ uint32_t scalar_code(const uint8_t* row, int d, int bits, int vpb) {
@@ -281,11 +297,14 @@ extern "C" int smaq_rotate_rows(const void* x, int xdtype, long long rows, int D
   SMAQ_REQUIRE(x && Mt && out, "smaq_rotate_rows: null pointer");
   SMAQ_REQUIRE(D > 0, "smaq_rotate_rows: bad head_dim");
   if (rows <= 0) return SMAQ_OK;
-  const int64_t n = (int64_t)rows * D;
+  SMAQ_REQUIRE(D <= 1024, "smaq_rotate_rows: head_dim above 1024");
+  const int64_t blocks = ((int64_t)rows + kRotRows - 1) / kRotRows;
+  SMAQ_REQUIRE(blocks < (1ll << 31), "smaq_rotate_rows: too many rows");
   hipStream_t st = (hipStream_t)stream;
   SMAQ_DISPATCH_DTYPE(xdtype, T,
-      hipLaunchKernelGGL(rotate_rows_kernel<T>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                         (const T*)x, (int64_t)rows, D, Mt, coord_scales, out);
+      hipLaunchKernelGGL(rotate_rows_kernel<T>, dim3((unsigned)blocks), dim3(D),
+                         (size_t)kRotRows * D * sizeof(float), st, (const T*)x, (int64_t)rows, D, Mt,
+                         coord_scales, out);
       return launch_status("smaq_rotate_rows");)
   set_error("smaq_rotate_rows: unsupported dtype %d", xdtype);
   return SMAQ_EUNSUPPORTED;

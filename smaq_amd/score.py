@@ -139,6 +139,7 @@ class AttentionPlan:
             p.recent_len = None if recent_len is None else recent_len.data_ptr()
             p.recent_batch_stride = rk.shape[1] * rk.shape[2] * rk.shape[3]
             p.max_recent_len = int(max_recent_len)
+        self.needs_exact = has_recent
         self.out = torch.empty(B, T, Hq, D, dtype=out_dtype, device=dev)
         p.out = self.out.data_ptr()
         p.out_dtype = _native.dtype_code(out_dtype)
@@ -150,10 +151,19 @@ class AttentionPlan:
         self._keep = keep
 
     def load_query(self, query: torch.Tensor) -> None:
-        """Copy a query in and prepare the codec-space query (rotate kernel)."""
-        self.q_exact.copy_(query.reshape(self.shape))
+        """Copy a query in and prepare the codec-space query.  With a rotated
+        codec the rotate kernel reads the query in its own dtype; the fp32 copy
+        is made only when the exact (recent-window) path or an unrotated
+        codec reads it."""
+        q = query.reshape(self.shape)
         if self.q_hist is not None:
-            _native.rotate_rows_into(self.q_exact, self.rot_t, self.rot_scale, self.q_hist)
+            if q.dtype not in (torch.float32, torch.float16, torch.bfloat16) or not q.is_contiguous():
+                q = q.to(torch.float32).contiguous()
+            _native.rotate_rows_into(q, self.rot_t, self.rot_scale, self.q_hist)
+            if self.needs_exact:
+                self.q_exact.copy_(q)
+        else:
+            self.q_exact.copy_(q)
 
     def launch(self, phases: int = 0) -> torch.Tensor:
         """Launch the attention phases (0 = all) on the current stream."""

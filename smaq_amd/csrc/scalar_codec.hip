@@ -15,7 +15,7 @@
 //    maps to the top code.
 #include <type_traits>
 
-#include "smaq_common.h"
+#include "encode_internal.h"
 
 namespace smaq {
 
@@ -23,20 +23,6 @@ constexpr int kEncRows = 8;     // rows per tile
 constexpr int kEncThreads = 256;
 constexpr int kMaxDim = 256;
 constexpr int kMaxBounds = 255;
-
-__device__ __forceinline__ int count_below(const float* bounds, int nb, float y, unsigned* ties) {
-  if (y != y) return nb;  // NaN -> searchsorted returns len
-  int c = 0;
-  bool tie = false;
-  for (int i = 0; i < nb; ++i) {
-    const float b = bounds[i];
-    c += (b < y) ? 1 : 0;
-    const float tol = 1e-6f * fmaxf(fmaxf(fabsf(b), fabsf(y)), 1e-6f);
-    tie |= fabsf(y - b) <= tol;
-  }
-  *ties += tie ? 1u : 0u;
-  return c;
-}
 
 template <typename T>
 __global__ __launch_bounds__(kEncThreads) void encode_scalar_kernel(
@@ -140,7 +126,6 @@ __global__ __launch_bounds__(kEncThreads) void encode_scalar_kernel(
   add_count(tie_count, ties);
 }
 
-// y[r][j] = (sum_d x[r][d] * Mt[d][j]) [* s[j]], sequential FMA over d.
 // out[r][j] = (sum_d x[r][d] * Mt[d][j]) [* s[j]], one sequential fmaf chain
 // over d per output (the reference's CPU matmul order).  A block holds
 // kRotRows rows in LDS and one thread per column j; each Mt element loaded
@@ -285,6 +270,9 @@ extern "C" int smaq_encode_scalar(const void* k, int kdtype, long long n_outer, 
   if (rows == 0) return SMAQ_OK;
   RowMap map{n_inner, s_outer, s_inner};
   hipStream_t st = (hipStream_t)stream;
+  if (encode_scalar_mfma_supported(D, bits, n_bounds, codes_out, k, kdtype, s_outer, s_inner))
+    return launch_encode_scalar_mfma(kdtype, k, map, rows, Mt, coord_scales, bounds, n_bounds, bits,
+                                     codes_out, norms_out, tie_count, st);
   SMAQ_DISPATCH_DTYPE(kdtype, T,
       return launch_encode<T>(k, map, rows, D, Mt, coord_scales, bounds, n_bounds, bits,
                               codes_out, norms_out, tie_count, st);)

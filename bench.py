@@ -211,6 +211,78 @@ def bench_paged(args, dev):
     }
 
 
+# -------------------------------------------------------------- prefill ---
+
+def bench_prefill(args, dev):
+    """c4: hybrid chunked prefill at Qwen2-7B shape: 28 query / 4 KV heads,
+    2048 causal queries over 65408 block-VQ history tokens (block_dim 2, 256
+    centroids = 4 bits/dim, 4 outlier channels x20) + 128 fp16 recent tokens,
+    2-bit values."""
+    import smaq_amd as S
+    from smaq_amd import _native
+    from smaq_amd.synthetic import sample_keys, sample_values
+
+    Hq, Hkv, D = 28, 4, 128
+    N, R, T = args.prefill_context - 128, 128, args.prefill_queries
+    g = torch.Generator().manual_seed(3)
+    outl = torch.randperm(D, generator=g)[:4]
+    calib_k = sample_keys(4096, seed=31)
+    calib_k[:, outl] *= 20
+    calib_q = sample_keys(4096, seed=32)
+    strat = S.SMAQBlockVQStrategy(D, block_dim=2, n_centroids=256, device=dev)
+    strat.quantizer.fit(calib_k, calib_q, kmeans_iters=args.fit_iters)
+    keys = sample_keys(N * Hkv, seed=33, device=dev, dtype=torch.float16).view(N, Hkv, D)
+    keys[..., outl.to(dev)] *= 20
+    vals = sample_values(N * Hkv, seed=34, device=dev, dtype=torch.float16).view(N, Hkv, D)
+    st = S.CompressedKVStore(D, Hkv, device=dev, key_strategy=strat)
+    st.append_chunk(keys, vals)
+    kr = sample_keys(R * Hkv, seed=35, device=dev, dtype=torch.float16).view(R, Hkv, D)
+    kr[..., outl.to(dev)] *= 20
+    vr = sample_values(R * Hkv, seed=36, device=dev, dtype=torch.float16).view(R, Hkv, D)
+    q = sample_keys(T * Hq, seed=37, device=dev, dtype=torch.float16).view(T, Hq, D)
+    pos = torch.arange(N + R - T, N + R, device=dev)
+
+    def step():
+        return S.compute_hybrid_attention(q, st, kr, vr, Hq, query_positions=pos)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    start, end = _events(2)
+    start.record()
+    for _ in range(args.steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    # QK + PV multiply-adds over the causal pairs, 2 flops each
+    pairs = sum(min(int(p) + 1, N + R) for p in pos.tolist()) * Hq
+    flops = pairs * D * 2 * 2
+    byts = N * Hkv * (64 + 32 + 8 + 8) + R * Hkv * D * 2 * 2 + T * Hq * D * 2 * 2
+    return {
+        "metric": METRIC,
+        "value": T / (ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded keys with 4 outlier channels x20, N(0,1) values)",
+        "config": {"workload": "c4 hybrid chunked prefill, Qwen2-7B shape", "q_heads": Hq, "kv_heads": Hkv,
+                   "head_dim": D, "queries": T, "history": N, "recent": R, "key_format": "block-VQ bd=2 nc=256",
+                   "value_bits": 2, "storage_dtype": "fp16", "causal": True},
+        "roofline": {"bound": "mfma", "achieved": flops / (ms * 1e-3) / 1e12, "peak": 2500.0,
+                     "unit": "TFLOP/s", "frac": flops / (ms * 1e-3) / 1e12 / 2500.0, "traffic": None,
+                     "kernel": "attn_hist_kernel+attn_recent_kernel", "algorithmic_flops": flops,
+                     "algorithmic_bytes": byts},
+        "cpu_baseline": None,
+    }
+
+
 # --------------------------------------------------------------- encode ---
 
 def bench_encode(args, dev):
@@ -387,7 +459,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="decode", choices=["decode", "encode", "paged"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "encode", "paged", "prefill"])
+    ap.add_argument("--prefill-context", type=int, default=65536, help="c4 context (history + 128 recent)")
+    ap.add_argument("--prefill-queries", type=int, default=2048, help="c4 causal query tokens")
     ap.add_argument("--paged-seqs", type=int, default=256, help="c5 sequences")
     ap.add_argument("--encode-tokens", type=int, default=32768, help="c2 tokens per sequence")
     ap.add_argument("--fit-samples", type=int, default=8192, help="c2 codebook calibration samples")
@@ -410,7 +484,7 @@ def main():
     if args.copy_probe:
         print(json.dumps(copy_ceiling(dev)), flush=True)
         return
-    res = {"encode": bench_encode, "paged": bench_paged}.get(args.workload, bench_decode)(args, dev)
+    res = {"encode": bench_encode, "paged": bench_paged, "prefill": bench_prefill}.get(args.workload, bench_decode)(args, dev)
     print(json.dumps(res), flush=True)
 
 

@@ -199,7 +199,10 @@ typedef struct smaq_attn_params {
   int phases;
   /* kernel choice: 0 = automatic (matrix-core decode kernel when the shape
      allows, generic kernels otherwise), 1 = generic kernels only, 2 = the
-     matrix-core decode kernel (SMAQ_EUNSUPPORTED if the shape does not fit). */
+     matrix-core decode kernel, 3 = the matrix-core prefill kernel
+     (SMAQ_EUNSUPPORTED if the shape does not fit).  Automatic choice: the
+     decode kernel for single-token queries, the prefill kernel for
+     q_len >= 16 at head_dim 128, the generic kernels otherwise. */
   int impl;
 } smaq_attn_params;
 

@@ -99,7 +99,7 @@ class QuantizedKVBatch:
         """query [B, Hq, D] (one decode token per sequence) or [B, T, Hq, D];
         recent_k/v [B, R, Hkv, D] with per-sequence recent_len.  Returns the
         query's shape in its dtype.  ``impl``: 0 automatic, 1 generic kernels,
-        2 matrix-core decode kernel."""
+        2 matrix-core decode kernel, 3 matrix-core prefill kernel."""
         out = self.plan(query, scale, recent_k, recent_v, recent_len, impl).run(query)
         return out.squeeze(1) if query.dim() == 3 else out
 
@@ -143,8 +143,12 @@ class PagedQuantizedKV:
         return cls(strategy, codes, norms, vd, vs, vz, block_table, [k.shape[0] for k in keys], block_size,
                    value_bits, value_group)
 
-    def plan(self, query: torch.Tensor, scale: Optional[float] = None, impl: int = 0) -> AttentionPlan:
-        q = query.unsqueeze(1)
+    def plan(self, query: torch.Tensor, scale: Optional[float] = None, impl: int = 0,
+             query_positions: Optional[torch.Tensor] = None) -> AttentionPlan:
+        """A reusable launch for queries shaped like ``query`` ([B, Hq, D] or
+        [B, T, Hq, D]); ``query_positions`` int64 [B, T] masks history token
+        j for query t when j > query_positions[b, t]."""
+        q = query.unsqueeze(1) if query.dim() == 3 else query
         D = q.shape[-1]
         scale = 1.0 / math.sqrt(D) if scale is None else scale
         return AttentionPlan(
@@ -152,15 +156,17 @@ class PagedQuantizedKV:
             val_data=self.v_data, val_scales=self.v_scales, val_zeros=self.v_zeros, val_bits=self.value_bits,
             val_group=self.value_group, n_kv_heads=self.num_kv_heads, hist_len=self.hist_len,
             max_hist_len=max(self.seq_lens), block_table=self.block_table, block_size=self.block_size,
-            scale=scale, out_dtype=query.dtype, impl=impl)
+            scale=scale, out_dtype=query.dtype, query_positions=query_positions, impl=impl)
 
     def nbytes_per_token_head(self) -> int:
         n = self.codes.shape[-1] + (self.norms.element_size() if self.norms is not None else 0)
         return n + self.v_data.shape[-1] + 2 * self.v_scales.shape[-1] * self.v_scales.element_size()
 
-    def attention(self, query: torch.Tensor, scale: Optional[float] = None, impl: int = 0) -> torch.Tensor:
-        """query [B, Hq, D] -> [B, Hq, D]."""
-        return self.plan(query, scale, impl).run(query).squeeze(1)
+    def attention(self, query: torch.Tensor, scale: Optional[float] = None, impl: int = 0,
+                  query_positions: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """query [B, Hq, D] -> [B, Hq, D], or [B, T, Hq, D] -> [B, T, Hq, D]."""
+        out = self.plan(query, scale, impl, query_positions).run(query)
+        return out.squeeze(1) if query.dim() == 3 else out
 
 
 def require_native() -> None:

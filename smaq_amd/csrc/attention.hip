@@ -354,15 +354,19 @@ struct Plan {
   int row_tiles;
   int64_t hist_split, recent_split;
   int s_hist, s_recent;
-  bool mfma;
+  bool mfma, prefill;
+  int64_t hist_lp, recent_lp;  // prefill plane lengths
 };
+
+static int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
 
 static Plan make_plan(const smaq_attn_params* p) {
   Plan pl;
   const int g = p->n_q_heads / p->n_kv_heads;
   const int rows = p->q_len * g;
   pl.row_tiles = (rows + kRowTile - 1) / kRowTile;
-  pl.mfma = p->impl != 1 && p->has_history && mfma_decode_supported(*p);
+  pl.mfma = (p->impl == 0 || p->impl == 2) && p->has_history && mfma_decode_supported(*p);
+  pl.prefill = (p->impl == 0 || p->impl == 3) && !pl.mfma && prefill_mfma_supported(*p);
   const int64_t units = (int64_t)p->batch * p->n_kv_heads * pl.row_tiles;
   // aim for >= 2048 workgroups over the history
   int64_t want = units >= 2048 ? 1 : (2048 + units - 1) / units;
@@ -372,9 +376,16 @@ static Plan make_plan(const smaq_attn_params* p) {
   if (split < 4 * kChunk) split = 4 * kChunk;
   if (pl.mfma) split = mfma_decode_split_len(*p);
   pl.hist_split = split;
-  pl.s_hist = hl > 0 ? (int)((hl + split - 1) / split) : 0;
   int64_t rl = p->has_recent ? p->max_recent_len : 0;
   pl.recent_split = 4 * kChunk;
+  pl.hist_lp = pl.recent_lp = 0;
+  if (pl.prefill) {
+    if (hl > 0) pl.hist_split = prefill_split_len(*p, hl);
+    if (rl > 0) pl.recent_split = prefill_split_len(*p, rl);
+    pl.hist_lp = prefill_padded_len(hl);
+    pl.recent_lp = prefill_padded_len(rl);
+  }
+  pl.s_hist = hl > 0 ? (int)((hl + pl.hist_split - 1) / pl.hist_split) : 0;
   pl.s_recent = rl > 0 ? (int)((rl + pl.recent_split - 1) / pl.recent_split) : 0;
   return pl;
 }
@@ -389,7 +400,13 @@ extern "C" long long smaq_attn_workspace_bytes(const smaq_attn_params* p) {
   const int64_t S = pl.s_hist + pl.s_recent;
   const int64_t rows = (int64_t)p->q_len * (p->n_q_heads / p->n_kv_heads);
   const int64_t n = (int64_t)p->batch * p->n_kv_heads * rows * (S > 0 ? S : 1);
-  return n * (p->head_dim + 2) * (long long)sizeof(float);
+  int64_t bytes = n * (p->head_dim + 2) * (int64_t)sizeof(float);
+  if (pl.prefill) {
+    // four f16 planes (key hi/lo, value hi/lo) per part
+    const int64_t per_tok = (int64_t)p->batch * p->n_kv_heads * p->head_dim * 4 * 2;
+    bytes = align256(bytes) + align256(pl.hist_lp * per_tok) + align256(pl.recent_lp * per_tok);
+  }
+  return bytes;
 }
 
 template <int KEY, typename TN, typename TV>
@@ -449,6 +466,11 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
     set_error("smaq_attn_hybrid: the matrix-core decode kernel does not serve this shape");
     return SMAQ_EUNSUPPORTED;
   }
+  if (p.impl == 3 && !pl.prefill) {
+    set_error("smaq_attn_hybrid: the matrix-core prefill kernel does not serve this shape");
+    return SMAQ_EUNSUPPORTED;
+  }
+  SMAQ_REQUIRE(p.impl >= 0 && p.impl <= 3, "smaq_attn_hybrid: unknown impl %d", p.impl);
   const long long need = smaq_attn_workspace_bytes(&p);
   SMAQ_REQUIRE(p.workspace_bytes >= need, "smaq_attn_hybrid: workspace %lld < %lld bytes",
                p.workspace_bytes, need);
@@ -463,7 +485,38 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
   part.o = part.l + n_part;
 
   const int phases = p.phases ? p.phases : 7;
-  if (pl.s_hist > 0 && (phases & 1)) {
+  if (pl.prefill) {
+    char* ws = (char*)p.workspace + align256(n_part * (p.head_dim + 2) * (int64_t)sizeof(float));
+    auto planes = [&](int64_t lp) {
+      const int64_t n_el = (int64_t)p.batch * p.n_kv_heads * p.head_dim * lp;
+      PrefillPlanes P;
+      P.kh = (_Float16*)ws;
+      P.kl = P.kh + n_el;
+      P.vh = P.kl + n_el;
+      P.vl = P.vh + n_el;
+      P.Lp = lp;
+      ws += align256(n_el * 4 * 2);
+      return P;
+    };
+    const PrefillPlanes hp = planes(pl.hist_lp);
+    const PrefillPlanes rp = planes(pl.recent_lp);
+    if (pl.s_hist > 0 && (phases & 1)) {
+      HistAddr a{p.hist_seq_start, p.max_hist_len, p.hist_head_stride, p.block_table, p.max_blocks,
+                 p.block_size, p.n_kv_heads};
+      int rc = launch_prefill_planes_hist(p, a, hp, st);
+      if (rc != SMAQ_OK) return rc;
+      const PrefillPart pp{p.q_hist, hp.kh, hp.kl, hp.vh, hp.vl, p.hist_len, p.max_hist_len, hp.Lp,
+                           pl.hist_split, p.hist_pos_offset, 0};
+      if ((rc = launch_prefill_mfma(p, pp, pl.s_hist, part, st)) != SMAQ_OK) return rc;
+    }
+    if (pl.s_recent > 0 && (phases & 2)) {
+      int rc = launch_prefill_planes_recent(p, rp, st);
+      if (rc != SMAQ_OK) return rc;
+      const PrefillPart pp{p.q_exact, rp.kh, rp.kl, rp.vh, rp.vl, p.recent_len, p.max_recent_len, rp.Lp,
+                           pl.recent_split, p.recent_pos_offset, pl.s_hist};
+      if ((rc = launch_prefill_mfma(p, pp, pl.s_recent, part, st)) != SMAQ_OK) return rc;
+    }
+  } else if (pl.s_hist > 0 && (phases & 1)) {
     HistAddr a{p.hist_seq_start, p.max_hist_len, p.hist_head_stride, p.block_table, p.max_blocks,
                p.block_size, p.n_kv_heads};
     int rc = SMAQ_EUNSUPPORTED;
@@ -483,7 +536,7 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
     if (rc != SMAQ_OK) return rc;
     if (!pl.mfma && (rc = launch_status("smaq_attn_hybrid(history)")) != SMAQ_OK) return rc;
   }
-  if (pl.s_recent > 0 && (phases & 2)) {
+  if (!pl.prefill && pl.s_recent > 0 && (phases & 2)) {
     dim3 grid(pl.s_recent, p.n_kv_heads * pl.row_tiles, p.batch);
     switch (p.recent_dtype) {
       case SMAQ_F32: hipLaunchKernelGGL(attn_recent_kernel<float>, grid, dim3(kAttnThreads), 0, st, p, part, pl.s_hist, pl.recent_split, pl.row_tiles); break;

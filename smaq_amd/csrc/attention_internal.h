@@ -32,6 +32,33 @@ struct Partials {
 
 
 
+// Matrix-core prefill path (attention_prefill.hip).  Each attended part
+// (history, recent window) is first decoded into f16 hi/lo planes:
+// keys [B][Hkv][Lp][128], values dimension-major [B][Hkv][128][Lp].
+struct PrefillPlanes {
+  _Float16 *kh, *kl, *vh, *vl;
+  int64_t Lp;  // padded tokens per (sequence, KV head), multiple of 64
+};
+
+// One part as the prefill kernel reads it.
+struct PrefillPart {
+  const float* q;               // q_hist or q_exact
+  const _Float16 *kh, *kl, *vh, *vl;
+  const long long* len;         // [batch] tokens per sequence, NULL: max_len
+  int64_t max_len, Lp, split_len;
+  long long pos_offset;         // absolute position of token 0
+  int s_base;                   // first partials split of this part
+};
+
+bool prefill_mfma_supported(const smaq_attn_params& p);
+int64_t prefill_padded_len(int64_t L);
+int64_t prefill_split_len(const smaq_attn_params& p, int64_t L);
+int launch_prefill_planes_hist(const smaq_attn_params& p, const HistAddr& a, const PrefillPlanes& pl,
+                               hipStream_t st);
+int launch_prefill_planes_recent(const smaq_attn_params& p, const PrefillPlanes& pl, hipStream_t st);
+int launch_prefill_mfma(const smaq_attn_params& p, const PrefillPart& pp, int n_splits, const Partials& part,
+                        hipStream_t st);
+
 // MFMA decode path (attention_mfma.hip).  Returns true when it can serve
 // these parameters (history only, decode shape, supported formats).
 bool mfma_decode_supported(const smaq_attn_params& p);

@@ -78,7 +78,7 @@ class AttentionPlan:
         p = _native.AttnParams()
         p.batch, p.q_len, p.n_q_heads, p.n_kv_heads, p.head_dim = B, T, Hq, n_kv_heads, D
         p.scale = float(scale)
-        p.impl = int(impl)   # 0 auto, 1 generic kernels, 2 matrix-core decode kernel
+        p.impl = int(impl)   # 0 auto, 1 generic, 2 matrix-core decode, 3 matrix-core prefill
         keep = []
         self.q_exact = torch.empty(B, T, Hq, D, dtype=torch.float32, device=dev)
         p.q_exact = self.q_exact.data_ptr()
@@ -213,6 +213,7 @@ def compute_hybrid_attention(
     num_query_heads: int,
     scale: Optional[float] = None,
     query_positions: Optional[torch.Tensor] = None,
+    impl: int = 0,
 ) -> torch.Tensor:
     """Attention of query [T, Hq, D] over the store's history and the exact
     recent window [R, Hkv, D] (smaq/score.py:23-72).
@@ -220,7 +221,8 @@ def compute_hybrid_attention(
     ``query_positions`` (int64 [T], optional) is an extension for chunked
     prefill: key j (history positions 0..N-1, then recent N..N+R-1) is visible
     to query t iff j <= query_positions[t].  None reproduces the reference,
-    which applies no mask.
+    which applies no mask.  ``impl`` picks the kernels (0 automatic,
+    1 generic, 2 matrix-core decode, 3 matrix-core prefill).
     """
     head_dim = store.head_dim
     hkv = store.num_kv_heads
@@ -257,7 +259,7 @@ def compute_hybrid_attention(
         recent_len=None, max_recent_len=recent_k.shape[0] if has_recent else 0,
         scale=scale, out_dtype=query.dtype,
         query_positions=None if query_positions is None else query_positions.reshape(1, -1),
-        hist_pos_offset=0, recent_pos_offset=n_all, **kw)
+        hist_pos_offset=0, recent_pos_offset=n_all, impl=impl, **kw)
     return out.squeeze(0)
 
 

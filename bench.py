@@ -42,6 +42,22 @@ def _cores() -> int:
     return torch.get_num_threads()
 
 
+def history_kernel_ms(plan, q, steps: int) -> float:
+    """Mean duration of the history-partials kernel alone: HIP events on the
+    plan's launch stream (torch's current stream) around `steps` back-to-back
+    launches of that phase (the query is loaded once; every launch recomputes
+    the same partials), so no host-side gap between launches is timed."""
+    plan.load_query(q)
+    plan.launch(phases=1)
+    a, b = _events(2)
+    a.record()
+    for _ in range(steps):
+        plan.launch(phases=1)
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
+
+
 # --------------------------------------------------------------- decode ---
 
 def bench_decode(args, dev):
@@ -81,15 +97,7 @@ def bench_decode(args, dev):
     ms_step = start.elapsed_time(end) / args.steps
     # dominant kernel: HIP events on its launch stream (torch's current
     # stream, which the plan launches on) around the history phase alone
-    ea, eb = _events(args.steps), _events(args.steps)
-    for i in range(args.steps):
-        plan.load_query(q)
-        ea[i].record()
-        plan.launch(phases=1)
-        eb[i].record()
-        plan.launch(phases=4)
-    torch.cuda.synchronize()
-    kern_ms = statistics.mean(a.elapsed_time(b) for a, b in zip(ea, eb))
+    kern_ms = history_kernel_ms(plan, q, args.steps)
     achieved = algo_bytes / (kern_ms * 1e-3) / 1e9
     traffic = recorded_traffic("decode_mfma_c3", dict(batch=B, context=N))
 
@@ -176,15 +184,7 @@ def bench_paged(args, dev):
     end.record()
     torch.cuda.synchronize()
     ms_step = start.elapsed_time(end) / args.steps
-    ea, eb = _events(args.steps), _events(args.steps)
-    for i in range(args.steps):
-        plan.load_query(q)
-        ea[i].record()
-        plan.launch(phases=1)
-        eb[i].record()
-        plan.launch(phases=4)
-    torch.cuda.synchronize()
-    kern_ms = statistics.mean(a.elapsed_time(b) for a, b in zip(ea, eb))
+    kern_ms = history_kernel_ms(plan, q, args.steps)
     achieved = algo / (kern_ms * 1e-3) / 1e9
     return {
         "metric": METRIC,
@@ -458,7 +458,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--workload", default="decode", choices=["decode", "encode", "paged", "prefill"])
     ap.add_argument("--prefill-context", type=int, default=65536, help="c4 context (history + 128 recent)")
     ap.add_argument("--prefill-queries", type=int, default=2048, help="c4 causal query tokens")

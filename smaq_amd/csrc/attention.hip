@@ -329,9 +329,11 @@ __global__ __launch_bounds__(kMaxHeadDim) void attn_combine_kernel(smaq_attn_par
   if (d >= D) return;
   const int64_t base = part.idx(b, h, p.n_kv_heads, rows, r, 0);
   float M = -__builtin_inff();
+#pragma unroll 8
   for (int s = 0; s < part.S; ++s)
     if (part.l[base + s] > 0.0f) M = fmaxf(M, part.m[base + s]);
   float L = 0.0f, oh = 0.0f, orc = 0.0f;
+#pragma unroll 8
   for (int s = 0; s < part.S; ++s) {
     const float l = part.l[base + s];
     if (!(l > 0.0f)) continue;
@@ -549,10 +551,11 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
   }
   if (!(phases & 4)) return SMAQ_OK;
   dim3 cgrid((unsigned)rows, p.n_kv_heads, p.batch);
+  const dim3 cblock((unsigned)((p.head_dim + 63) / 64 * 64));  // one thread per output dim
   switch (p.out_dtype) {
-    case SMAQ_F32: hipLaunchKernelGGL(attn_combine_kernel<float>, cgrid, dim3(kMaxHeadDim), 0, st, p, part, pl.s_hist); break;
-    case SMAQ_F16: hipLaunchKernelGGL(attn_combine_kernel<_Float16>, cgrid, dim3(kMaxHeadDim), 0, st, p, part, pl.s_hist); break;
-    case SMAQ_BF16: hipLaunchKernelGGL(attn_combine_kernel<bf16>, cgrid, dim3(kMaxHeadDim), 0, st, p, part, pl.s_hist); break;
+    case SMAQ_F32: hipLaunchKernelGGL(attn_combine_kernel<float>, cgrid, cblock, 0, st, p, part, pl.s_hist); break;
+    case SMAQ_F16: hipLaunchKernelGGL(attn_combine_kernel<_Float16>, cgrid, cblock, 0, st, p, part, pl.s_hist); break;
+    case SMAQ_BF16: hipLaunchKernelGGL(attn_combine_kernel<bf16>, cgrid, cblock, 0, st, p, part, pl.s_hist); break;
     default: set_error("smaq_attn_hybrid: unsupported output dtype %d", p.out_dtype); return SMAQ_EUNSUPPORTED;
   }
   return launch_status("smaq_attn_hybrid(combine)");

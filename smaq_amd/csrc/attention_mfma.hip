@@ -4,14 +4,17 @@
 // (two per byte), 2-bit values in groups of 32, one query token per sequence
 // and up to 4 query heads per KV head.  One workgroup = 4 waves over one
 // (context split, KV head, sequence); each wave streams 32-token tiles, and
-// loads the next tile's rows while it computes the current one.
+// issues each array's loads for the next tile as soon as it has consumed the
+// current tile's copy.  With 16-bit norms and value metadata the kernel fits
+// 128 VGPRs, i.e. 4 waves per SIMD (the query operands live in LDS).
 //
 // Per 32-token tile (two 16-token halves):
 //   QK   v_mfma_f32_16x16x32_f16, M = 16 tokens, K = 32 dims, N = 16 columns:
 //        columns [0, Q) hold the query hi parts, [8, 8+Q) the lo parts.  The
 //        decoded key is split hi/lo as well (q.k ~= qh.kh + ql.kh + qh.kl), so
 //        scores keep ~22 bits against fp32.  Key bytes (two codes) go through
-//        a 256-entry LDS table that returns both codes' f16 hi and lo halves.
+//        a 256-entry LDS table whose 8-byte entries hold both codes' f16 hi
+//        and lo halves (one ds_read_b64 per byte).
 //   soft the hi and lo columns are summed with one DPP add and the 4 x 32
 //        (query, token) scores are redistributed two per lane; online softmax
 //        in base 2 whose reference maximum is raised only when a score exceeds
@@ -28,6 +31,8 @@
 // unsupported shapes use the generic kernels in attention.hip.
 #include <math.h>
 
+#include <type_traits>
+
 #include "attention_internal.h"
 
 namespace smaq {
@@ -38,6 +43,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kMWaves = 4;
 constexpr int kMTile = 32;
@@ -107,12 +113,17 @@ __device__ __forceinline__ float dpp_row_ror(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xf, 0xf, true));
 }
 
-// (x & m) | c in one instruction (m in an SGPR, c in a VGPR).
-__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t c) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(m), "v"(c));
-  return r;
+// Raw buffer descriptor of a wave-uniform base address (no stride, no range
+// limit): loads through it take the base from SGPRs and a 32-bit lane offset.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, -1, 0x00020000);
 }
+
+// (x & m) | c.  Plain code, not inline asm, so that the compiler sees the VALU
+// write and keeps the wait states the matrix core needs before reading the
+// result as an operand; with m in an SGPR and c in a VGPR it is one
+// v_and_or_b32.
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t c) { return (x & m) | c; }
 
 // Two consecutive storage-dtype values -> fp32 (one 4- or 8-byte load; the
 // element index must be even).
@@ -144,6 +155,14 @@ struct Pack8 {
       w[4] = c.x; w[5] = c.y; w[6] = c.z; w[7] = c.w;
     }
   }
+  __device__ __forceinline__ void load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    w[0] = a[0]; w[1] = a[1]; w[2] = a[2]; w[3] = a[3];
+    if constexpr (sizeof(T) == 4) {
+      const u32x4 c = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16, 0, 0);
+      w[4] = c[0]; w[5] = c[1]; w[6] = c[2]; w[7] = c[3];
+    }
+  }
   __device__ __forceinline__ void set(int i, T v) {  // element-wise fill
     if constexpr (sizeof(T) == 2) {
       const uint32_t bits = (uint32_t)__builtin_bit_cast(uint16_t, v);
@@ -160,17 +179,60 @@ struct Pack8 {
   }
 };
 
-template <int KBITS, typename TN, typename TV>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void decode_mfma_kernel(
+// Waves per SIMD of the decode kernel: 4 (<= 128 VGPRs) with 16-bit norms and
+// value metadata; 3 when either is fp32 (more registers per tile).
+template <typename TN, typename TV>
+constexpr int kDecodeWaves = (sizeof(TN) == 2 && sizeof(TV) == 2) ? 4 : 3;
+
+// Two consecutive key norms, kept as loaded and widened on use.
+template <typename T>
+struct NormPair {
+  uint32_t w[sizeof(T) == 2 ? 1 : 2];
+  __device__ __forceinline__ void load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+    // (a second dword load: this toolchain lowers raw_buffer_load_b64 to one dword)
+    if constexpr (sizeof(T) == 4) w[1] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 4, 0);
+  }
+  __device__ __forceinline__ void load(const T* p) {  // element index even
+    if constexpr (sizeof(T) == 2) {
+      w[0] = *(const uint32_t*)p;
+    } else {
+      const uint2 v = *(const uint2*)p;
+      w[0] = v.x; w[1] = v.y;
+    }
+  }
+  __device__ __forceinline__ void set(int i, T v) {
+    if constexpr (sizeof(T) == 2) {
+      const uint32_t bits = (uint32_t)__builtin_bit_cast(uint16_t, v);
+      w[0] = i ? ((w[0] & 0xffffu) | (bits << 16)) : ((w[0] & 0xffff0000u) | bits);
+    } else {
+      w[i] = __builtin_bit_cast(uint32_t, v);
+    }
+  }
+  __device__ __forceinline__ float get(int i) const {
+    if constexpr (sizeof(T) == 2)
+      return Num<T>::to_f(__builtin_bit_cast(T, (uint16_t)(w[0] >> (16 * i))));
+    else
+      return __builtin_bit_cast(float, w[i]);
+  }
+};
+
+template <int KBITS, typename TN, typename TV, bool SPLIT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWaves<TN, TV>, kDecodeWaves<TN, TV>))) void decode_mfma_kernel(
     smaq_attn_params p, HistAddr addr, Partials part, int64_t split_len) {
-  __shared__ uint32_t lut[2][256];  // [0]: f16 hi pair, [1]: f16 lo pair
+  // key LUT, one 8-byte entry per code byte: {f16 hi pair, f16 lo pair}
+  // (read with ds_read_b64, twice the rate of two dword reads)
+  __shared__ __attribute__((aligned(16))) u32x2 lut[256];
+  // query B operands (one u32x4 per lane and K step), shared by the 4 waves
+  __shared__ __attribute__((aligned(16))) u32x4 bqs[8][64];
   // per wave: value codes spread to 16 bits ([code byte][token pair] dwords)
   // and the PV A operand ([row][hi 32 tokens | lo 32 tokens] bf16)
   __shared__ __attribute__((aligned(16))) uint8_t vsp[kMWaves][32 * kVRow];
   __shared__ __attribute__((aligned(16))) uint8_t ast[kMWaves][16 * kARow];
   __shared__ float red_m[kMWaves][4];
   __shared__ float red_l[kMWaves][4];
-  __shared__ float red_o[kMWaves][4][128];
+  // per-wave results, laid over the spread tiles once every wave has left its loop
+  float (*const red_o)[4][128] = (float (*)[4][128])&vsp[0][0];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
@@ -196,8 +258,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     const float c1 = p.key_lut[(v >> KBITS) & kMask] * lut_scale;
     const _Float16 h0 = (_Float16)c0, h1 = (_Float16)c1;
     const _Float16 l0 = (_Float16)(c0 - (float)h0), l1 = (_Float16)(c1 - (float)h1);
-    lut[0][v] = f16_bits(h0) | (f16_bits(h1) << 16);
-    lut[1][v] = f16_bits(l0) | (f16_bits(l1) << 16);
+    lut[v] = u32x2{f16_bits(h0) | (f16_bits(h1) << 16), f16_bits(l0) | (f16_bits(l1) << 16)};
   }
 
   // ---- query B operands: columns [0, Q) hold the hi parts of query rows
@@ -220,26 +281,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   // [hi(d0) hi(d1) lo(d0) lo(d1) hi(d2) hi(d3) lo(d2) lo(d3)] (two LUT pairs).
   // x = q hi (columns < Q) or q lo (columns 8..8+Q), y = q hi (columns < Q), so
   // column j + column 8+j = qh.kh + qh.kl + ql.kh.
-  u32x4 bq[8];
+  if (w == 0) {
 #pragma unroll
-  for (int st = 0; st < 8; ++st) {
-    uint32_t xw[2], yw[2];
+    for (int st = 0; st < 8; ++st) {
+      uint32_t xw[2], yw[2];
 #pragma unroll
-    for (int pr2 = 0; pr2 < 2; ++pr2) {
-      uint32_t xx = 0, yy = 0;
+      for (int pr2 = 0; pr2 < 2; ++pr2) {
+        uint32_t xx = 0, yy = 0;
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const float x = qv[4 * st + 2 * pr2 + hh] * q_scale;
-        const _Float16 hi = (_Float16)x;
-        const _Float16 lo = (_Float16)(x - (float)hi);
-        const uint32_t hb = f16_bits(hi), lb = f16_bits(lo);
-        xx |= (n < Q ? hb : (qrow >= 0 ? lb : 0u)) << (16 * hh);
-        yy |= (n < Q ? hb : 0u) << (16 * hh);
+        for (int hh = 0; hh < 2; ++hh) {
+          const float x = qv[4 * st + 2 * pr2 + hh] * q_scale;
+          const _Float16 hi = (_Float16)x;
+          const _Float16 lo = (_Float16)(x - (float)hi);
+          const uint32_t hb = f16_bits(hi), lb = f16_bits(lo);
+          xx |= (n < Q ? hb : (qrow >= 0 ? lb : 0u)) << (16 * hh);
+          yy |= (n < Q ? hb : 0u) << (16 * hh);
+        }
+        xw[pr2] = xx;
+        yw[pr2] = yy;
       }
-      xw[pr2] = xx;
-      yw[pr2] = yy;
+      bqs[st][lane] = u32x4{xw[0], yw[0], xw[1], yw[1]};
     }
-    bq[st] = u32x4{xw[0], yw[0], xw[1], yw[1]};
   }
   // score factor of query row qq: scale * log2(e) * 2^(e_q + e_lut), taken
   // from column qq (its hi column)
@@ -267,7 +329,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   f32x4 acc_s = {0.f, 0.f, 0.f, 0.f};  // sum of A per row (query kg, group v)
   float zacc[4] = {0.f, 0.f, 0.f, 0.f};  // this lane's share of sum p * zero, query qq
   const u32x4 kOnesBf16 = u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
-  const uint32_t kBf16Base = 0x43004300u;  // bf16 128.0 in both halves
+  // bf16 128.0 in both halves, and the four 2-bit field masks of a spread
+  // code byte; hidden from constant folding so that each B operand dword is a
+  // single v_and_or_b32 (mask from an SGPR, base from a VGPR) rather than an
+  // and plus an or with two literals
+  uint32_t bf16_base = 0x43004300u;
+  asm volatile("" : "+v"(bf16_base));
+  uint32_t fmask[4] = {0x00030003u, 0x000c000cu, 0x00300030u, 0x00600060u};
+#pragma unroll
+  for (int f = 0; f < 4; ++f) asm volatile("" : "+s"(fmask[f]));
 
   // LDS addresses (lane constants)
   uint8_t* const vw = &vsp[w][kVRow * 4 * pq + 8 * tq];       // spread writer, code byte 4pq
@@ -309,29 +379,49 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     const int c = min(i, d.last);
     return c < 16 ? d.gA + c : d.gB + (c - 16);
   };
-  // this lane's first softmax token row (tokens tokA, tokA + 1 are consecutive rows)
-  auto rowA = [&](const TileDesc& d) -> int64_t { return tokA < 16 ? d.gA + tokA : d.gB + (tokA - 16); };
 
-  // Full tiles with even rows: vector loads, the same instructions for every
-  // tile (so the pipelined loop below waits on exact load counts).
+  // Full tiles with even rows.  Without SPLIT the second 16-token group
+  // follows the first (gB = gA + 16): every array is read through a buffer
+  // descriptor of the tile's first row (SGPRs) plus a constant lane offset, so
+  // a tile costs no vector address arithmetic.  With SPLIT (16-token pages)
+  // the lanes of the second group read from another block and take 64-bit
+  // row addresses.
+  const uint32_t offK = (uint32_t)(n * 64 + 16 * kg);
+  const uint32_t offV = (uint32_t)(128 * tq + 4 * pq);  // rows 4tq.. (both groups when gB = gA + 16)
   auto fast_values = [&](const TileDesc& d, uint32_t* vd) {
-    const uint8_t* vrow = vbytes + ((tq < 4 ? d.gA : d.gB) + 4 * (tq & 3)) * 32 + 4 * pq;
+    if constexpr (SPLIT) {
+      const uint8_t* vrow = vbytes + ((tq < 4 ? d.gA : d.gB) + 4 * (tq & 3)) * 32 + 4 * pq;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) vd[i] = *(const uint32_t*)(vrow + 32 * i);
+      for (int i = 0; i < 4; ++i) vd[i] = *(const uint32_t*)(vrow + 32 * i);
+    } else {
+      const auto rv = buf_rsrc(vbytes + d.gA * 32);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vd[i] = __builtin_amdgcn_raw_buffer_load_b32(rv, offV, 32 * i, 0);
+    }
   };
   auto fast_keys = [&](const TileDesc& d, u32x4& kqa, u32x4& kqb) {
-    const uint32_t off = (uint32_t)(n * 64 + 16 * kg);
-    kqa = *(const u32x4*)(kbytes + d.gA * 64 + off);
-    kqb = *(const u32x4*)(kbytes + d.gB * 64 + off);
+    kqa = __builtin_amdgcn_raw_buffer_load_b128(buf_rsrc(kbytes + d.gA * 64), offK, 0, 0);
+    kqb = __builtin_amdgcn_raw_buffer_load_b128(buf_rsrc(kbytes + d.gB * 64), offK, 0, 0);
   };
-  auto fast_norms = [&](const TileDesc& d, float* nrm) { load2<TN>(norms + rowA(d), nrm); };
+  // this lane's first softmax token row (tokens tokA, tokA + 1 are consecutive rows)
+  auto rowA = [&](const TileDesc& d) -> int64_t { return tokA < 16 ? d.gA + tokA : d.gB + (tokA - 16); };
+  auto fast_norms = [&](const TileDesc& d, NormPair<TN>& nrm) {
+    if constexpr (SPLIT) nrm.load(norms + rowA(d));
+    else nrm.load_buf(buf_rsrc(norms + d.gA), (uint32_t)(tokA * sizeof(TN)));
+  };
   auto fast_side = [&](const TileDesc& d, Pack8<TV>& sv, Pack8<TV>& zv) {
-    const int64_t r = rowA(d);
-    sv.load(vsc + r * 4);
-    zv.load(vzr + r * 4);
+    if constexpr (SPLIT) {
+      const int64_t r = rowA(d);
+      sv.load(vsc + r * 4);
+      zv.load(vzr + r * 4);
+    } else {
+      const uint32_t o = (uint32_t)(tokA * 4 * sizeof(TV));
+      sv.load_buf(buf_rsrc(vsc + d.gA * 4), o);
+      zv.load_buf(buf_rsrc(vzr + d.gA * 4), o);
+    }
   };
   // Any tile (tail or odd rows): element loads with clamped rows.
-  auto slow_loads = [&](const TileDesc& d, u32x4& kqa, u32x4& kqb, uint32_t* vd, float* nrm,
+  auto slow_loads = [&](const TileDesc& d, u32x4& kqa, u32x4& kqb, uint32_t* vd, NormPair<TN>& nrm,
                         Pack8<TV>& sv, Pack8<TV>& zv) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) vd[i] = *(const uint32_t*)(vbytes + rowof(d, 4 * tq + i) * 32 + 4 * pq);
@@ -340,7 +430,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int64_t r = rowof(d, tokA + i);
-      nrm[i] = Num<TN>::to_f(norms[r]);
+      nrm.set(i, norms[r]);
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         sv.set(4 * i + g, vsc[r * 4 + g]);
@@ -352,11 +442,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   float m_thr = -__builtin_inff();  // m_run + kLazyRescale
   // One tile.  The hooks run right after the tile's copy of the matching
   // registers has been consumed (the pipelined loop loads the next tile there).
-  auto tile = [&](const TileDesc& dcur, u32x4& kqa, u32x4& kqb, uint32_t* vd, float* nrm,
+  auto tile = [&](auto tail_tag, int last, u32x4& kqa, u32x4& kqb, uint32_t* vd, NormPair<TN>& nrm,
                   Pack8<TV>& sv, Pack8<TV>& zv, auto&& after_values, auto&& after_keys,
                   auto&& after_norms, auto&& after_side) {
-    const int last = dcur.last;
-    const bool tail = last < 31;
+    constexpr bool TAIL = decltype(tail_tag)::value;
     // -- value codes spread to 16 bits: dword (byte j, tokens 2i, 2i+1) =
     // [code byte of token 2i, 0, code byte of token 2i+1, 0]
 #pragma unroll
@@ -370,15 +459,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     after_values();
     // -- QK: per step two key bytes -> two LUT pairs -> one A operand
     f32x4 ca = {0.f, 0.f, 0.f, 0.f}, cb = {0.f, 0.f, 0.f, 0.f};
+    typedef const __attribute__((address_space(3))) u32x4 LdsU32x4;
+    const LdsU32x4* bqp = (const LdsU32x4*)&bqs[0][lane];
+    asm volatile("" : "+v"(bqp));  // read each tile (keeps the operands out of registers)
 #pragma unroll
     for (int st = 0; st < 8; ++st) {
+      const u32x4 bqv = bqp[64 * st];
       const uint32_t wa = kqa[st >> 1] >> (16 * (st & 1)), wb = kqb[st >> 1] >> (16 * (st & 1));
       const uint32_t a0 = wa & 0xffu, a1 = (wa >> 8) & 0xffu;
       const uint32_t b0 = wb & 0xffu, b1 = (wb >> 8) & 0xffu;
-      const u32x4 av = u32x4{lut[0][a0], lut[1][a0], lut[0][a1], lut[1][a1]};
-      const u32x4 bv = u32x4{lut[0][b0], lut[1][b0], lut[0][b1], lut[1][b1]};
-      ca = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(av), as_f16x8(bq[st]), ca, 0, 0, 0);
-      cb = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(bv), as_f16x8(bq[st]), cb, 0, 0, 0);
+      const u32x2 pa0 = lut[a0], pa1 = lut[a1], pb0 = lut[b0], pb1 = lut[b1];
+      const u32x4 av = u32x4{pa0[0], pa0[1], pa1[0], pa1[1]};
+      const u32x4 bv = u32x4{pb0[0], pb0[1], pb1[0], pb1[1]};
+      ca = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(av), as_f16x8(bqv), ca, 0, 0, 0);
+      cb = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(bv), as_f16x8(bqv), cb, 0, 0, 0);
     }
     after_keys();
     // -- scores.  C layout: lane (kg, n) holds column n for tokens 4kg + v (ca)
@@ -397,10 +491,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     x1 = dpp_bank_move<0x118, 0x4>(x1, sc[5]);
     x0 = dpp_bank_move<0x11c, 0x8>(x0, sc[6]);  // row_shr:12 into bank 3
     x1 = dpp_bank_move<0x11c, 0x8>(x1, sc[7]);
-    x0 *= nrm[0];  // score / rfac (rfac > 0 is applied in the exponent)
-    x1 *= nrm[1];
+    x0 *= nrm.get(0);  // score / rfac (rfac > 0 is applied in the exponent)
+    x1 *= nrm.get(1);
     after_norms();
-    if (tail) {
+    if constexpr (TAIL) {
       if (tokA > last) x0 = -__builtin_inff();
       if (tokA + 1 > last) x1 = -__builtin_inff();
     }
@@ -429,9 +523,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     }
     // exp2(-inf) = 0 covers masked tokens; only a row with no valid token yet
     // (m_run = -inf, possible in a tail tile) needs the guard against inf - inf
-    const bool dead = tail && m_run == -__builtin_inff();
-    const float p0 = dead ? 0.0f : fast_exp2(fmaf(x0, rfac, -m_run));
-    const float p1 = dead ? 0.0f : fast_exp2(fmaf(x1, rfac, -m_run));
+    float p0, p1;
+    if constexpr (TAIL) {
+      const bool dead = m_run == -__builtin_inff();
+      p0 = dead ? 0.0f : fast_exp2(fmaf(x0, rfac, -m_run));
+      p1 = dead ? 0.0f : fast_exp2(fmaf(x1, rfac, -m_run));
+    } else {
+      p0 = fast_exp2(fmaf(x0, rfac, -m_run));
+      p1 = fast_exp2(fmaf(x1, rfac, -m_run));
+    }
     l_run += p0 + p1;
     // -- PV A operand (row (qq, g), tokens tokA, tokA + 1): p * scale split into
     // a bf16 hi part (truncation, exact remainder) and a rounded bf16 lo part
@@ -466,8 +566,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
       u32x4 bv;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        bv[i] = f < 3 ? and_or(wv[i], 0x00030003u << (2 * f), kBf16Base)
-                      : and_or(wv[i] >> 1, 0x00600060u, kBf16Base);
+        bv[i] = f < 3 ? and_or(wv[i], fmask[f], bf16_base) : and_or(wv[i] >> 1, fmask[3], bf16_base);
       acc_o[tau] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ahi), as_bf16x8(bv), acc_o[tau], 0, 0, 0);
       acc_o[tau] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(alo), as_bf16x8(bv), acc_o[tau], 0, 0, 0);
     }
@@ -476,14 +575,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 
   u32x4 kqa, kqb;
   uint32_t vd[4];
-  float nrm[2];
+  NormPair<TN> nrm;
   Pack8<TV> sv, zv;
   auto none = [] {};
   int64_t t0 = s0 + (int64_t)wu * kMTile;
   // Pipelined loop over full tiles with even rows (paged rows always are;
   // contiguous rows when the head's first row is even).  Each iteration
-  // issues the next tile's loads as soon as this tile's registers are free,
-  // so every load has one iteration to arrive; the last iteration reloads its
+  // issues the next tile's loads once this tile's registers are consumed, so
+  // every load has one iteration to arrive; the last iteration reloads its
   // own rows (cache hits) to keep the load sequence identical.
   const bool even_rows = paged || (contig_base & 1) == 0;
   if (even_rows && t0 + kMTile <= s1) {
@@ -497,9 +596,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
       const int64_t tn = t0 + kMWaves * kMTile;
       const bool more = __builtin_amdgcn_readfirstlane((int)(tn + kMTile <= s1)) != 0;
       const TileDesc dn = more ? describe(tn) : dc;
-      tile(dc, kqa, kqb, vd, nrm, sv, zv,
-           [&] { fast_values(dn, vd); }, [&] { fast_keys(dn, kqa, kqb); },
-           [&] { fast_norms(dn, nrm); }, [&] { fast_side(dn, sv, zv); });
+      tile(std::false_type{}, 31, kqa, kqb, vd, nrm, sv, zv, [&] { fast_values(dn, vd); },
+           [&] { fast_keys(dn, kqa, kqb); }, [&] { fast_norms(dn, nrm); }, [&] { fast_side(dn, sv, zv); });
       t0 = tn;
       dc = dn;
       if (!more) break;
@@ -510,7 +608,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     t0 = uniform64(t0);
     const TileDesc d = describe(t0);
     slow_loads(d, kqa, kqb, vd, nrm, sv, zv);
-    tile(d, kqa, kqb, vd, nrm, sv, zv, none, none, none, none);
+    tile(std::true_type{}, d.last, kqa, kqb, vd, nrm, sv, zv, none, none, none, none);
   }
 
   // ---- per-wave result.  Sum the per-lane shares of query qq (banks, rows).
@@ -528,6 +626,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     z += __shfl_xor(z, 32, 64);
     zq[g] = __shfl(z, kg, 64);  // query kg
   }
+  __syncthreads();  // red_o overlays the spread tiles of every wave
   if (kg < Q) {
     // C element (row (kg, g), column n) of step tau: dim 4 * (16 * (tau & 1) + n) + (tau >> 1),
     // which lies in group g = 2 * (tau & 1) + (n >> 3)
@@ -590,24 +689,32 @@ int64_t mfma_decode_split_len(const smaq_attn_params& p) {
   return split < 4 * q ? 4 * q : split;
 }
 
-template <int KB, typename TN>
+template <int KB, typename TN, bool SPLIT>
 static void launch_v(const smaq_attn_params& p, const HistAddr& a, const Partials& part,
                      int64_t split_len, int n_splits, hipStream_t st) {
   dim3 grid(n_splits, p.n_kv_heads, p.batch);
   switch (p.val_dtype) {
-    case SMAQ_F32: hipLaunchKernelGGL((decode_mfma_kernel<KB, TN, float>), grid, dim3(256), 0, st, p, a, part, split_len); break;
-    case SMAQ_F16: hipLaunchKernelGGL((decode_mfma_kernel<KB, TN, _Float16>), grid, dim3(256), 0, st, p, a, part, split_len); break;
-    default: hipLaunchKernelGGL((decode_mfma_kernel<KB, TN, bf16>), grid, dim3(256), 0, st, p, a, part, split_len); break;
+    case SMAQ_F32: hipLaunchKernelGGL((decode_mfma_kernel<KB, TN, float, SPLIT>), grid, dim3(256), 0, st, p, a, part, split_len); break;
+    case SMAQ_F16: hipLaunchKernelGGL((decode_mfma_kernel<KB, TN, _Float16, SPLIT>), grid, dim3(256), 0, st, p, a, part, split_len); break;
+    default: hipLaunchKernelGGL((decode_mfma_kernel<KB, TN, bf16, SPLIT>), grid, dim3(256), 0, st, p, a, part, split_len); break;
   }
+}
+
+template <int KB, typename TN>
+static void launch_s(const smaq_attn_params& p, const HistAddr& a, const Partials& part,
+                     int64_t split_len, int n_splits, hipStream_t st) {
+  // 16-token pages put a tile's two 16-token groups in different blocks
+  if (p.block_table && p.block_size == 16) launch_v<KB, TN, true>(p, a, part, split_len, n_splits, st);
+  else launch_v<KB, TN, false>(p, a, part, split_len, n_splits, st);
 }
 
 template <int KB>
 static void launch_n(const smaq_attn_params& p, const HistAddr& a, const Partials& part,
                      int64_t split_len, int n_splits, hipStream_t st) {
   switch (p.norm_dtype) {
-    case SMAQ_F32: launch_v<KB, float>(p, a, part, split_len, n_splits, st); break;
-    case SMAQ_F16: launch_v<KB, _Float16>(p, a, part, split_len, n_splits, st); break;
-    default: launch_v<KB, bf16>(p, a, part, split_len, n_splits, st); break;
+    case SMAQ_F32: launch_s<KB, float>(p, a, part, split_len, n_splits, st); break;
+    case SMAQ_F16: launch_s<KB, _Float16>(p, a, part, split_len, n_splits, st); break;
+    default: launch_s<KB, bf16>(p, a, part, split_len, n_splits, st); break;
   }
 }
 

@@ -132,6 +132,34 @@ __global__ __launch_bounds__(kEncThreads) void encode_scalar_kernel(
 // feeds kRotRows independent chains.
 constexpr int kRotRows = 8;
 
+// The same product for head_dim 128 with one thread per output element, so
+// that a decode step's few thousand query rows fill the GPU: a block holds 2
+// rows (staged in LDS, read as broadcasts) and each thread runs its column's
+// fmaf chain with the Mt loads issued 32 ahead.
+template <typename T>
+__global__ __launch_bounds__(256) void rotate_rows128_kernel(const T* __restrict__ x, int64_t rows,
+                                                             const float* __restrict__ Mt,
+                                                             const float* __restrict__ s,
+                                                             float* __restrict__ out) {
+  __shared__ float xs[2][128];
+  const int t = threadIdx.x;
+  const int rr = t >> 7, j = t & 127;
+  const int64_t r = (int64_t)blockIdx.x * 2 + rr;
+  xs[rr][j] = r < rows ? Num<T>::to_f(x[r * 128 + j]) : 0.0f;
+  __syncthreads();
+  if (r >= rows) return;
+  float acc = 0.0f;
+#pragma unroll
+  for (int d0 = 0; d0 < 128; d0 += 32) {
+    float m[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) m[i] = Mt[(d0 + i) * 128 + j];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) acc = fmaf(xs[rr][d0 + i], m[i], acc);
+  }
+  out[r * 128 + j] = s ? acc * s[j] : acc;
+}
+
 template <typename T>
 __global__ __launch_bounds__(1024) void rotate_rows_kernel(const T* __restrict__ x, int64_t rows,
                                                            int D, const float* __restrict__ Mt,
@@ -289,6 +317,15 @@ extern "C" int smaq_rotate_rows(const void* x, int xdtype, long long rows, int D
   const int64_t blocks = ((int64_t)rows + kRotRows - 1) / kRotRows;
   SMAQ_REQUIRE(blocks < (1ll << 31), "smaq_rotate_rows: too many rows");
   hipStream_t st = (hipStream_t)stream;
+  if (D == 128) {
+    SMAQ_REQUIRE((rows + 1) / 2 < (1ll << 31), "smaq_rotate_rows: too many rows");
+    SMAQ_DISPATCH_DTYPE(xdtype, T,
+        hipLaunchKernelGGL(rotate_rows128_kernel<T>, dim3((unsigned)((rows + 1) / 2)), dim3(256), 0, st,
+                           (const T*)x, (int64_t)rows, Mt, coord_scales, out);
+        return launch_status("smaq_rotate_rows");)
+    set_error("smaq_rotate_rows: unsupported dtype %d", xdtype);
+    return SMAQ_EUNSUPPORTED;
+  }
   SMAQ_DISPATCH_DTYPE(xdtype, T,
       hipLaunchKernelGGL(rotate_rows_kernel<T>, dim3((unsigned)blocks), dim3(D),
                          (size_t)kRotRows * D * sizeof(float), st, (const T*)x, (int64_t)rows, D, Mt,

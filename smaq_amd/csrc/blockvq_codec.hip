@@ -13,7 +13,7 @@
 //    sqrt comparison is only evaluated for such near-equal records.  (torch's
 //    vectorised sqrt is itself not correctly rounded; where that decides the
 //    winner the two distances are within 1 ulp -- a counted tie.)
-#include "smaq_common.h"
+#include "encode_internal.h"
 
 namespace smaq {
 
@@ -137,6 +137,9 @@ extern "C" int smaq_encode_blockvq(const void* k, int kdtype, long long n_outer,
   if (rows == 0) return SMAQ_OK;
   RowMap map{n_inner, s_outer, s_inner};
   hipStream_t st = (hipStream_t)stream;
+  if (encode_blockvq_mfma_supported(n_blocks, block_dim, n_centroids, k, kdtype, s_outer, s_inner))
+    return launch_encode_blockvq_mfma(kdtype, k, map, rows, n_blocks, E_blocks, centroids,
+                                      (uint8_t*)idx_out, tie_count, st);
   const size_t lds = (size_t)n_blocks * n_centroids * sizeof(float);
   const unsigned grid = (unsigned)((rows + kVqThreads - 1) / kVqThreads);
   switch (kdtype) {

@@ -30,4 +30,13 @@ int launch_encode_scalar_mfma(int kdtype, const void* k, RowMap map, int64_t row
                               const float* cs, const float* bounds, int nb, int bits, void* codes,
                               void* norms, unsigned long long* ties, hipStream_t st);
 
+// Matrix-core block-VQ encoder (blockvq_encode_mfma.hip): 8-dim blocks, 256
+// centroids, at most 16 blocks, 16-byte aligned key rows.
+bool encode_blockvq_mfma_supported(int nb, int bd, int nc, const void* k, int kdtype,
+                                   long long s_outer, long long s_inner);
+size_t encode_blockvq_mfma_lds(int nb);
+int launch_encode_blockvq_mfma(int kdtype, const void* k, RowMap map, int64_t rows, int nb,
+                               const float* E_blocks, const float* C, uint8_t* idx,
+                               unsigned long long* ties, hipStream_t st);
+
 }  // namespace smaq

@@ -185,6 +185,92 @@ def test_blockvq_encode_parity(dev, dtype, bd):
     assert torch.equal(k_hat, R.blockvq_dequantize(R.BlockQ(got, 128 // bd, bd), Dc))
 
 
+def _check_vq_against_oracle(idx_gpu, ref, keys, Eb, C, ties, what):
+    """Indices equal the oracle's except at counted argmin ties (distances
+    within 1e-6 relative of each other)."""
+    mism = idx_gpu != ref
+    n_mis = int(mism.sum())
+    if n_mis:
+        d = R.blockvq_distances(keys, Eb, C)
+        r_idx = mism.nonzero()
+        dg = d[r_idx[:, 0], r_idx[:, 1], idx_gpu[mism]]
+        dr = d[r_idx[:, 0], r_idx[:, 1], ref[mism]]
+        assert bool(((dg - dr).abs() <= 1e-6 * dr.clamp_min(1e-30)).all()), f"{what}: mismatch beyond a tie"
+    print(f"\n[{what}] index mismatches={n_mis} argmin-ties(gpu)={ties}")
+    assert n_mis <= ties
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_blockvq_encode_matrix_core_large(dev, dtype):
+    """The matrix-core encoder (8-dim blocks, 256 centroids) on 40,000 rows:
+    about 1e-3 of the (row, block) pairs take its exact recount, so this
+    covers both paths against the oracle; the rows also go through the
+    store's [T, Hkv, D] transpose view (strided row map)."""
+    Eb, Eib, C, Dc = _vq_setup(seed=3)
+    vq = S.SMAQBlockVQ(128, block_dim=8, device=dev)
+    vq.E_blocks, vq.E_inv_blocks = Eb.to(dev), Eib.to(dev)
+    vq.centroids, vq.decoded_centroids = C.to(dev), Dc.to(dev)
+    keys = sample_keys(40000, seed=57).to(dtype)
+    ref = R.blockvq_encode(keys, Eb, C).indices
+    vq.tie_counter = _native.TieCounter(dev)
+    got = vq.quantize(keys.to(dev)).indices.cpu().long()
+    _check_vq_against_oracle(got, ref, keys, Eb, C, vq.tie_counter.value(), f"blockvq mfma {dtype}")
+    kv = keys.reshape(10000, 4, 128)
+    vq.tie_counter = _native.TieCounter(dev)
+    got_v = vq.quantize(_store_view(kv.to(dev))).indices.cpu().long()   # [1, 4, T, 16]
+    assert torch.equal(got_v[0].transpose(0, 1).reshape(40000, 16), got)
+
+
+def test_blockvq_encode_exact_ties(dev):
+    """Constructed ties: duplicated centroids (exactly equal distances, the
+    first index wins), keys shaped onto midpoints of two centroids (distances
+    equal up to rounding: the exact recount decides as the reference does and
+    counts the tie) and a row with a NaN (the first index wins, not counted)."""
+    Eb, Eib, C, Dc = _vq_setup(seed=4)
+    C = C.clone()
+    C[:, 200] = C[:, 7]          # exact duplicates: index 7 must win over 200
+    C[:, 201] = C[:, 90]
+    nb = C.shape[0]
+    g = torch.Generator().manual_seed(91)
+    rows = 600
+    x = torch.empty(rows, nb, 8)
+    for b in range(nb):
+        a = torch.randint(0, 256, (rows,), generator=g)
+        c2 = torch.randint(0, 256, (rows,), generator=g)
+        mid = 0.5 * (C[b, a] + C[b, c2])
+        x[:, b] = torch.where((torch.arange(rows) % 3 == 0)[:, None], C[b, 7] + 1e-3 * torch.randn(rows, 8, generator=g), mid)
+    # keys whose shaped blocks are x: k_b = x_b E_b^-T
+    keys = torch.cat([x[:, b] @ torch.linalg.inv(Eb[b]).T for b in range(nb)], dim=1).float()
+    keys[5, 17] = float("nan")
+    vq = S.SMAQBlockVQ(128, block_dim=8, device=dev)
+    vq.E_blocks, vq.E_inv_blocks = Eb.to(dev), Eib.to(dev)
+    vq.centroids, vq.decoded_centroids = C.to(dev), Dc.to(dev)
+    ref = R.blockvq_encode(keys, Eb, C).indices
+    vq.tie_counter = _native.TieCounter(dev)
+    got = vq.quantize(keys.to(dev)).indices.cpu().long()
+    ties = vq.tie_counter.value()
+    fin = torch.isfinite(keys).all(dim=1)
+    # These distances tie up to rounding, and the reference's own rounding is
+    # host dependent: torch's CPU matmul for the cdist form sums its 10 terms
+    # in an order that depends on the CPU's SIMD kernels (this build's oracle
+    # host and the GPU host differ), shifting d2 by a few ulps of |x|^2 + |c|^2
+    # -- many ulps of d2 itself.  A differing index must be a tie under that
+    # bound, computed in float64 from the oracle's shaped keys.
+    kf, gf, rf = keys[fin], got[fin], ref[fin]
+    mism = (gf != rf).nonzero()
+    for r, b in mism.tolist():
+        xb = (kf[r:r + 1, 8 * b:8 * b + 8] @ Eb[b].T)[0].double()
+        cg, cr = C[b, gf[r, b]].double(), C[b, rf[r, b]].double()
+        d2g, d2r = ((xb - cg) ** 2).sum(), ((xb - cr) ** 2).sum()
+        bound = 32 * 2.0 ** -24 * (2 * (xb * xb).sum() + (cg * cg).sum() + (cr * cr).sum())
+        assert abs(float(d2g - d2r)) <= float(bound), f"row {r} block {b}: {float(d2g)} vs {float(d2r)}"
+    print(f"\n[blockvq constructed ties] index differences={len(mism)} (all within the rounding bound) "
+          f"argmin-ties(gpu)={ties}")
+    assert torch.equal(got[~fin][:, 2], ref[~fin][:, 2])      # NaN block: first index (0)
+    assert int(got[~fin][0, 2]) == 0
+    assert ties > 0
+
+
 def test_blockvq_fit_matches_oracle(dev):
     keys = sample_keys(2048, seed=90)
     queries = sample_keys(2048, seed=91)

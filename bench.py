@@ -203,7 +203,9 @@ def bench_paged(args, dev):
                    "head_dim": D, "key_bits": 3, "value_bits": 2, "value_group": 32, "storage_dtype": "bf16",
                    "total_tokens": int(lens.sum()), "physical_blocks": total},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "decode_mfma_kernel",
+                     "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": recorded_traffic("decode_mfma_paged_c5", dict(seqs=B, total_tokens=int(lens.sum()))),
+                     "kernel": "decode_mfma_kernel",
                      "kernel_ms": kern_ms, "algorithmic_bytes": algo,
                      "bytes_per_token_head": pk.nbytes_per_token_head()},
         "cpu_baseline": None,
@@ -241,9 +243,12 @@ def bench_prefill(args, dev):
     vr = sample_values(R * Hkv, seed=36, device=dev, dtype=torch.float16).view(R, Hkv, D)
     q = sample_keys(T * Hq, seed=37, device=dev, dtype=torch.float16).view(T, Hq, D)
     pos = torch.arange(N + R - T, N + R, device=dev)
+    from smaq_amd.score import plan_hybrid_attention
+    plan = plan_hybrid_attention(q, st, kr, vr, Hq, query_positions=pos)
+    q1 = q.unsqueeze(0)
 
     def step():
-        return S.compute_hybrid_attention(q, st, kr, vr, Hq, query_positions=pos)
+        return plan.run(q1)
 
     for _ in range(args.warmup):
         step()
@@ -255,9 +260,14 @@ def bench_prefill(args, dev):
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.steps
+    # history phase alone (block-VQ keys -> f16 planes, then the matrix-core
+    # kernel), events on its launch stream
+    kern_ms = history_kernel_ms(plan, q1, args.steps)
     # QK + PV multiply-adds over the causal pairs, 2 flops each
     pairs = sum(min(int(p) + 1, N + R) for p in pos.tolist()) * Hq
     flops = pairs * D * 2 * 2
+    hist_pairs = sum(min(int(p) + 1, N) for p in pos.tolist()) * Hq
+    hist_flops = hist_pairs * D * 2 * 2
     byts = N * Hkv * (64 + 32 + 8 + 8) + R * Hkv * D * 2 * 2 + T * Hq * D * 2 * 2
     return {
         "metric": METRIC,
@@ -275,10 +285,11 @@ def bench_prefill(args, dev):
         "config": {"workload": "c4 hybrid chunked prefill, Qwen2-7B shape", "q_heads": Hq, "kv_heads": Hkv,
                    "head_dim": D, "queries": T, "history": N, "recent": R, "key_format": "block-VQ bd=2 nc=256",
                    "value_bits": 2, "storage_dtype": "fp16", "causal": True},
-        "roofline": {"bound": "mfma", "achieved": flops / (ms * 1e-3) / 1e12, "peak": 2500.0,
-                     "unit": "TFLOP/s", "frac": flops / (ms * 1e-3) / 1e12 / 2500.0, "traffic": None,
-                     "kernel": "attn_hist_kernel+attn_recent_kernel", "algorithmic_flops": flops,
-                     "algorithmic_bytes": byts},
+        "roofline": {"bound": "mfma", "achieved": hist_flops / (kern_ms * 1e-3) / 1e12, "peak": 2500.0,
+                     "unit": "TFLOP/s", "frac": hist_flops / (kern_ms * 1e-3) / 1e12 / 2500.0, "traffic": None,
+                     "kernel": "prefill_mfma_kernel (history phase, with decode_hist_planes_kernel)",
+                     "kernel_ms": kern_ms, "algorithmic_flops": hist_flops, "step_flops": flops,
+                     "step_tflops": flops / (ms * 1e-3) / 1e12, "algorithmic_bytes": byts},
         "cpu_baseline": None,
     }
 
@@ -353,7 +364,7 @@ def bench_encode(args, dev):
                      "achieved": rows * 16 * 256 * 8 * 2 / (k_ms * 1e-3) / 1e12,
                      "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": rows * 16 * 256 * 8 * 2 / (k_ms * 1e-3) / 1e12 / FP32_PEAK_TFLOPS,
-                     "traffic": None, "pack_values_ms": v_ms,
+                     "traffic": recorded_traffic("encode_blockvq_c2", dict(rows=rows)), "pack_values_ms": v_ms,
                      "hbm_gbs": algo / ((k_ms + v_ms) * 1e-3) / 1e9, "algorithmic_bytes": algo,
                      "algorithmic_flops": flops},
         "cpu_baseline": cpu,
@@ -414,7 +425,7 @@ def recorded_traffic(name: str, config: dict):
     rec = {}
     with open(path) as f:
         for line in f:
-            if "=" in line and line.strip().startswith(("traffic_bytes_per_launch", "batch", "context")):
+            if "=" in line and line.strip().startswith(("traffic_bytes_per_launch", *config)):
                 k, v = line.split("=", 1)
                 rec[k.strip()] = int(v.strip())
     if "traffic_bytes_per_launch" not in rec or any(rec.get(k) != v for k, v in config.items()):
@@ -464,8 +475,8 @@ def main():
     ap.add_argument("--prefill-queries", type=int, default=2048, help="c4 causal query tokens")
     ap.add_argument("--paged-seqs", type=int, default=256, help="c5 sequences")
     ap.add_argument("--encode-tokens", type=int, default=32768, help="c2 tokens per sequence")
-    ap.add_argument("--fit-samples", type=int, default=8192, help="c2 codebook calibration samples")
-    ap.add_argument("--fit-iters", type=int, default=5, help="c2 Lloyd iterations")
+    ap.add_argument("--fit-samples", type=int, default=65536, help="c2 codebook calibration samples")
+    ap.add_argument("--fit-iters", type=int, default=20, help="c2/c4 Lloyd iterations")
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--context", type=int, default=32768)
     ap.add_argument("--no-cpu-baseline", action="store_true")

@@ -205,6 +205,56 @@ def _flat_tensors(flat: FlatCache):
     return [None if t is None else t.contiguous() for t in tensors], flat.num_tokens
 
 
+def plan_hybrid_attention(
+    query: torch.Tensor,
+    store: CompressedKVStore,
+    recent_k: Optional[torch.Tensor],
+    recent_v: Optional[torch.Tensor],
+    num_query_heads: int,
+    scale: Optional[float] = None,
+    query_positions: Optional[torch.Tensor] = None,
+    impl: int = 0,
+) -> Optional[AttentionPlan]:
+    """The fused launch ``compute_hybrid_attention`` makes for these inputs,
+    prepared but not run (a caller that repeats the same shape re-runs it);
+    None when the reference semantics need no fused launch (nothing to attend,
+    or a strategy without a fused kernel description)."""
+    head_dim = store.head_dim
+    hkv = store.num_kv_heads
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim)
+    flat = store.get_flat_cache()
+    has_history = flat is not None and flat.num_tokens >= MIN_HISTORY_FOR_SMAQ
+    has_recent = recent_k is not None and recent_k.shape[0] > 0
+    if not has_history and not has_recent:
+        return None
+    if num_query_heads % hkv:
+        raise ValueError(f"num_query_heads {num_query_heads} not a multiple of num_kv_heads {hkv}")
+    fused = None
+    if has_history:
+        fh = getattr(store.quantizer, "fused_history", None)
+        fused = fh() if fh is not None else None
+        if fused is None:
+            return None
+    n_all = flat.num_tokens if flat is not None else 0
+    if has_history:
+        (codes, norms, vdata, vsc, vz), stride = _flat_tensors(flat)
+        kw = dict(key_codes=codes, key_norms=norms, val_data=vdata, val_scales=vsc, val_zeros=vz,
+                  hist_head_stride=stride, max_hist_len=flat.num_tokens)
+    else:
+        kw = dict(key_codes=None, key_norms=None, val_data=None, val_scales=None, val_zeros=None,
+                  max_hist_len=0)
+    return AttentionPlan(
+        query=query.unsqueeze(0), fused=fused, val_bits=store.value_bits, val_group=store.value_group_size,
+        n_kv_heads=hkv, hist_len=None,
+        recent_k=recent_k.unsqueeze(0) if has_recent else None,
+        recent_v=recent_v.unsqueeze(0) if has_recent else None,
+        recent_len=None, max_recent_len=recent_k.shape[0] if has_recent else 0,
+        scale=scale, out_dtype=query.dtype,
+        query_positions=None if query_positions is None else query_positions.reshape(1, -1),
+        hist_pos_offset=0, recent_pos_offset=n_all, impl=impl, **kw)
+
+
 def compute_hybrid_attention(
     query: torch.Tensor,
     store: CompressedKVStore,
@@ -224,43 +274,18 @@ def compute_hybrid_attention(
     which applies no mask.  ``impl`` picks the kernels (0 automatic,
     1 generic, 2 matrix-core decode, 3 matrix-core prefill).
     """
-    head_dim = store.head_dim
-    hkv = store.num_kv_heads
-    if scale is None:
-        scale = 1.0 / math.sqrt(head_dim)
+    plan = plan_hybrid_attention(query, store, recent_k, recent_v, num_query_heads, scale, query_positions, impl)
+    if plan is not None:
+        return plan.run(query.unsqueeze(0)).squeeze(0)
     flat = store.get_flat_cache()
     has_history = flat is not None and flat.num_tokens >= MIN_HISTORY_FOR_SMAQ
     has_recent = recent_k is not None and recent_k.shape[0] > 0
     if not has_history and not has_recent:
-        return torch.zeros(query.shape[0], num_query_heads, head_dim, device=query.device, dtype=query.dtype)
-    if num_query_heads % hkv:
-        raise ValueError(f"num_query_heads {num_query_heads} not a multiple of num_kv_heads {hkv}")
-    fused = None
-    if has_history:
-        fh = getattr(store.quantizer, "fused_history", None)
-        fused = fh() if fh is not None else None
-        if fused is None:
-            return _generic_hybrid(query, store, flat, recent_k, recent_v, num_query_heads, scale,
-                                   has_recent, query_positions)
-    n_all = flat.num_tokens if flat is not None else 0
-    kw = {}
-    if has_history:
-        (codes, norms, vdata, vsc, vz), stride = _flat_tensors(flat)
-        kw = dict(key_codes=codes, key_norms=norms, val_data=vdata, val_scales=vsc, val_zeros=vz,
-                  hist_head_stride=stride, max_hist_len=flat.num_tokens)
-    else:
-        kw = dict(key_codes=None, key_norms=None, val_data=None, val_scales=None, val_zeros=None,
-                  max_hist_len=0)
-    out = launch_fused_attention(
-        query=query.unsqueeze(0), fused=fused, val_bits=store.value_bits, val_group=store.value_group_size,
-        n_kv_heads=hkv, hist_len=None,
-        recent_k=recent_k.unsqueeze(0) if has_recent else None,
-        recent_v=recent_v.unsqueeze(0) if has_recent else None,
-        recent_len=None, max_recent_len=recent_k.shape[0] if has_recent else 0,
-        scale=scale, out_dtype=query.dtype,
-        query_positions=None if query_positions is None else query_positions.reshape(1, -1),
-        hist_pos_offset=0, recent_pos_offset=n_all, impl=impl, **kw)
-    return out.squeeze(0)
+        return torch.zeros(query.shape[0], num_query_heads, store.head_dim, device=query.device, dtype=query.dtype)
+    if num_query_heads % store.num_kv_heads:
+        raise ValueError(f"num_query_heads {num_query_heads} not a multiple of num_kv_heads {store.num_kv_heads}")
+    return _generic_hybrid(query, store, flat, recent_k, recent_v, num_query_heads,
+                           1.0 / math.sqrt(store.head_dim) if scale is None else scale, has_recent, query_positions)
 
 
 def _generic_hybrid(query, store, flat, recent_k, recent_v, num_query_heads, scale, has_recent,

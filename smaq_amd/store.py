@@ -90,6 +90,7 @@ class CompressedKVStore:
         self._cols: dict[str, _Column] = {}
         self._n = 0
         self._key_meta: Optional[tuple] = None
+        self._mem_bytes = 0
 
     @property
     def capabilities(self) -> CacheCapabilities:
@@ -110,17 +111,25 @@ class CompressedKVStore:
         v = value.transpose(0, 1).unsqueeze(0)
         key_q = self.key_strategy.quantize(k)
         val_q = quantize_values(v, bits=self.value_bits, group_size=self.value_group_size)
-        self._key_chunks.append(key_q)
-        self._value_chunks.append(val_q)
+        self._mem_bytes += self.key_strategy.memory_bytes(key_q) + _value_bytes(val_q)
         self._chunk_lengths.append(chunk_len)
-        self._append_columns(key_q, val_q)
+        if self._append_columns(key_q, val_q):
+            # the columns hold the chunk; the chunk tensors are released
+            self._key_chunks.clear()
+            self._value_chunks.clear()
+        else:
+            self._key_chunks.append(key_q)
+            self._value_chunks.append(val_q)
         self._flat = None
 
-    def _append_columns(self, key_q: Any, val_q: ValueQuantized) -> None:
+    def _append_columns(self, key_q: Any, val_q: ValueQuantized) -> bool:
+        """Copy the chunk into the columns; False (columns dropped) for key
+        layouts they do not handle."""
         fields = _key_fields(key_q)
-        if fields is None:
-            self._cols = {}
-            return
+        if fields is None or (self._n and not self._cols):
+            if self._cols:
+                raise ValueError("key chunks of different layouts in one store")
+            return False
         meta, tensors = fields
         if self._key_meta is not None and self._key_meta != meta:
             raise ValueError("key chunks of different layouts in one store")
@@ -133,10 +142,11 @@ class CompressedKVStore:
         for name, t in tensors.items():
             self._cols.setdefault(name, _Column()).append(t, n_old)
         self._n = n_old + tensors["v_data"].shape[1]
+        return True
 
     def get_flat_cache(self) -> Optional[FlatCache]:
         """Head-major flattened history (smaq/store.py:97-114)."""
-        if not self._key_chunks:
+        if not self._chunk_lengths:
             return None
         if self._flat is not None:
             return self._flat
@@ -165,13 +175,9 @@ class CompressedKVStore:
         return self._flat
 
     def memory_bytes(self) -> int:
-        """16-bit metadata accounting (smaq/store.py:116-124)."""
-        total = 0
-        for kq in self._key_chunks:
-            total += self.key_strategy.memory_bytes(kq)
-        for vq in self._value_chunks:
-            total += vq.data.nelement() + vq.scales.nelement() * 2 + vq.zeros.nelement() * 2
-        return total
+        """Per-chunk key bytes plus value bytes with 16-bit metadata, summed
+        over the appended chunks (smaq/store.py:116-124)."""
+        return self._mem_bytes
 
     def reset(self):
         self._key_chunks.clear()
@@ -181,6 +187,7 @@ class CompressedKVStore:
         self._cols = {}
         self._n = 0
         self._key_meta = None
+        self._mem_bytes = 0
 
 
 def _key_fields(key_q: Any):
@@ -198,6 +205,11 @@ def _key_fields(key_q: Any):
         ind = key_q.indices
         return ("block_vq", key_q.n_blocks, key_q.block_dim), {"k_codes": ind.reshape(-1, *ind.shape[-2:])}
     return None
+
+
+def _value_bytes(vq: ValueQuantized) -> int:
+    """Value bytes of a chunk, metadata counted at 2 bytes (smaq/store.py:120-123)."""
+    return vq.data.nelement() + vq.scales.nelement() * 2 + vq.zeros.nelement() * 2
 
 
 def _flatten_value_q(value_q: ValueQuantized) -> ValueQuantized:

@@ -579,13 +579,48 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
   Pack8<TV> sv, zv;
   auto none = [] {};
   int64_t t0 = s0 + (int64_t)wu * kMTile;
-  // Pipelined loop over full tiles with even rows (paged rows always are;
+  // Pipelined loops over full tiles with even rows (paged rows always are;
   // contiguous rows when the head's first row is even).  Each iteration
   // issues the next tile's loads once this tile's registers are consumed, so
   // every load has one iteration to arrive; the last iteration reloads its
   // own rows (cache hits) to keep the load sequence identical.
   const bool even_rows = paged || (contig_base & 1) == 0;
-  if (even_rows && t0 + kMTile <= s1) {
+  // Contiguous rows: the split's full 128-token steps (one 32-token tile per
+  // wave) in a rotated order whose start differs between workgroups.  Every
+  // split starts at the same offset of its sequence's arrays, so without the
+  // rotation concurrent workgroups stream the same address phase; measured on
+  // MI355X, the rotation alone takes the load stream from 5.6 to 5.9 TB/s.
+  // The next row is formed without a branch: with a branch at the loop top
+  // the compiler waits for every load of the tile there instead of for each
+  // array when it is first used.
+  const int64_t n_steps = (s1 - s0) / (kMWaves * kMTile);
+  if (!paged && even_rows && n_steps > 0) {
+    constexpr int64_t kStep = kMWaves * kMTile;
+    const int K = __builtin_amdgcn_readfirstlane((int)n_steps);
+    const int r = __builtin_amdgcn_readfirstlane(
+        (int)((blockIdx.x * 7u + blockIdx.y * 13u + blockIdx.z * 5u) % (unsigned)K));
+    const int64_t base = uniform64(contig_base + s0 + (int64_t)wu * kMTile);  // step 0 of this wave
+    const int64_t wrap = (int64_t)K * kStep;
+    const int64_t rot_end = base + wrap;
+    int64_t row = uniform64(base + (int64_t)r * kStep);
+    const TileDesc dc{row, row + 16, 31};
+    fast_values(dc, vd);
+    fast_keys(dc, kqa, kqb);
+    fast_norms(dc, nrm);
+    fast_side(dc, sv, zv);
+    for (int i = 0;;) {
+      ++i;
+      const bool more = i < K;
+      int64_t rn = row + (more ? kStep : 0);
+      rn = uniform64(rn >= rot_end ? rn - wrap : rn);
+      const TileDesc dn{rn, rn + 16, 31};
+      tile(std::false_type{}, 31, kqa, kqb, vd, nrm, sv, zv, [&] { fast_values(dn, vd); },
+           [&] { fast_keys(dn, kqa, kqb); }, [&] { fast_norms(dn, nrm); }, [&] { fast_side(dn, sv, zv); });
+      row = rn;
+      if (!more) break;
+    }
+    t0 += n_steps * kStep;
+  } else if (even_rows && t0 + kMTile <= s1) {
     TileDesc dc = describe(t0);
     fast_values(dc, vd);
     fast_keys(dc, kqa, kqb);

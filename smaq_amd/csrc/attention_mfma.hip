@@ -620,6 +620,50 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
       if (!more) break;
     }
     t0 += n_steps * kStep;
+  } else if (paged && t0 + kMTile <= s1) {
+    // Paged rows: a counted loop over this wave's full tiles.  The block
+    // table entries of a tile are loaded (scalar loads) one iteration before
+    // its rows are formed, so the loop never waits on a table lookup, and
+    // the row is (block * Hkv + h) << log2(block_size) + offset with the
+    // block-times-head product in 32 bits (the pool has < 2^32 block-heads).
+    constexpr int64_t kStep = kMWaves * kMTile;
+    const int K = __builtin_amdgcn_readfirstlane((int)((s1 - t0 - kMTile) / kStep + 1));
+    const uint32_t t_first = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)t0);
+    const uint32_t bmask = (uint32_t)bsz - 1u;
+    auto entries = [&](int k, uint32_t& ea, uint32_t& eb) {
+      const uint32_t t = t_first + (uint32_t)k * (uint32_t)kStep;
+      ea = (uint32_t)__builtin_amdgcn_readfirstlane(tbl[t >> bshift]);
+      eb = (uint32_t)__builtin_amdgcn_readfirstlane(tbl[(t + 16u) >> bshift]);
+    };
+    auto rows_of = [&](int k, uint32_t ea, uint32_t eb) -> TileDesc {
+      const uint32_t t = t_first + (uint32_t)k * (uint32_t)kStep;
+      const int64_t ga = (int64_t)((uint64_t)(ea * (uint32_t)n_kv + (uint32_t)h) << bshift) + (int64_t)(t & bmask);
+      const int64_t gb = (int64_t)((uint64_t)(eb * (uint32_t)n_kv + (uint32_t)h) << bshift) +
+                         (int64_t)((t + 16u) & bmask);
+      return TileDesc{uniform64(ga), uniform64(gb), 31};
+    };
+    uint32_t ea, eb, na, nb;
+    entries(0, ea, eb);
+    const TileDesc d0 = rows_of(0, ea, eb);
+    fast_values(d0, vd);
+    fast_keys(d0, kqa, kqb);
+    fast_norms(d0, nrm);
+    fast_side(d0, sv, zv);
+    entries(K > 1 ? 1 : 0, na, nb);  // the tile after the first
+    for (int i = 0;;) {
+      ++i;
+      const bool more = i < K;
+      const int kn = more ? i : i - 1;   // the last tile reloads its own rows
+      const TileDesc dn = rows_of(kn, na, nb);
+      uint32_t fa, fb;
+      entries(i + 1 < K ? i + 1 : K - 1, fa, fb);  // one more tile ahead
+      tile(std::false_type{}, 31, kqa, kqb, vd, nrm, sv, zv, [&] { fast_values(dn, vd); },
+           [&] { fast_keys(dn, kqa, kqb); }, [&] { fast_norms(dn, nrm); }, [&] { fast_side(dn, sv, zv); });
+      na = fa;
+      nb = fb;
+      if (!more) break;
+    }
+    t0 += (int64_t)K * kStep;
   } else if (even_rows && t0 + kMTile <= s1) {
     TileDesc dc = describe(t0);
     fast_values(dc, vd);

@@ -492,10 +492,7 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
     auto planes = [&](int64_t lp) {
       const int64_t n_el = (int64_t)p.batch * p.n_kv_heads * p.head_dim * lp;
       PrefillPlanes P;
-      P.kh = (_Float16*)ws;
-      P.kl = P.kh + n_el;
-      P.vh = P.kl + n_el;
-      P.vl = P.vh + n_el;
+      P.img = (_Float16*)ws;
       P.Lp = lp;
       ws += align256(n_el * 4 * 2);
       return P;
@@ -507,15 +504,15 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
                  p.block_size, p.n_kv_heads};
       int rc = launch_prefill_planes_hist(p, a, hp, st);
       if (rc != SMAQ_OK) return rc;
-      const PrefillPart pp{p.q_hist, hp.kh, hp.kl, hp.vh, hp.vl, p.hist_len, p.max_hist_len, hp.Lp,
-                           pl.hist_split, p.hist_pos_offset, 0};
+      const PrefillPart pp{p.q_hist, hp.img, p.hist_len, p.max_hist_len, hp.Lp, pl.hist_split,
+                           p.hist_pos_offset, 0};
       if ((rc = launch_prefill_mfma(p, pp, pl.s_hist, part, st)) != SMAQ_OK) return rc;
     }
     if (pl.s_recent > 0 && (phases & 2)) {
       int rc = launch_prefill_planes_recent(p, rp, st);
       if (rc != SMAQ_OK) return rc;
-      const PrefillPart pp{p.q_exact, rp.kh, rp.kl, rp.vh, rp.vl, p.recent_len, p.max_recent_len, rp.Lp,
-                           pl.recent_split, p.recent_pos_offset, pl.s_hist};
+      const PrefillPart pp{p.q_exact, rp.img, p.recent_len, p.max_recent_len, rp.Lp, pl.recent_split,
+                           p.recent_pos_offset, pl.s_hist};
       if ((rc = launch_prefill_mfma(p, pp, pl.s_recent, part, st)) != SMAQ_OK) return rc;
     }
   } else if (pl.s_hist > 0 && (phases & 1)) {

@@ -33,17 +33,18 @@ struct Partials {
 
 
 // Matrix-core prefill path (attention_prefill.hip).  Each attended part
-// (history, recent window) is first decoded into f16 hi/lo planes:
-// keys [B][Hkv][Lp][128], values dimension-major [B][Hkv][128][Lp].
+// (history, recent window) is first decoded into f16 hi/lo tile images:
+// [B][Hkv][Lp / 64] tiles of 64 KB, each the LDS image the kernel copies
+// (key hi, key lo, value hi, value lo; layout in attention_prefill.hip).
 struct PrefillPlanes {
-  _Float16 *kh, *kl, *vh, *vl;
+  _Float16* img;
   int64_t Lp;  // padded tokens per (sequence, KV head), multiple of 64
 };
 
 // One part as the prefill kernel reads it.
 struct PrefillPart {
   const float* q;               // q_hist or q_exact
-  const _Float16 *kh, *kl, *vh, *vl;
+  const _Float16* img;
   const long long* len;         // [batch] tokens per sequence, NULL: max_len
   int64_t max_len, Lp, split_len;
   long long pos_offset;         // absolute position of token 0

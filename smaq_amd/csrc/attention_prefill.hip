@@ -1,13 +1,25 @@
 // Chunked-prefill attention on the gfx950 matrix cores (head_dim 128).
 //
 // Prefill is compute-bound (every key tile serves many query rows), so the
-// packed cache is first decoded once per part into f16 hi/lo planes in the
-// workspace (the dequantisation the generic kernels do per query tile):
+// packed cache is first decoded once per part into f16 hi/lo tile images in
+// the workspace (the dequantisation the generic kernels do per query tile):
 //   keys   K~[t][d]  = lut[code] * norm (scalar) or decoded centroid (block-VQ);
 //                      the recent window's exact keys
 //   values V^[d][t]  = code * scale + zero (fp32, as the reference's
 //                      dequantize_values), stored dimension-major
 // each as hi = f16(x), lo = f16(x - hi), ~22 significant bits.
+//
+// Tile image (64 tokens of one (sequence, KV head), 64 KB, exactly what the
+// kernel holds in LDS):
+//   [K hi | K lo]  64 key rows x 256 B; 16-byte unit u (dims 8u..8u+7) of
+//                  row r sits at unit u ^ (r & 15)
+//   [V hi | V lo]  128 dim rows x 128 B; unit u = 4 st + kg holds keys
+//                  32 st + 4 kg + {0..3} and 32 st + 16 + 4 kg + {0..3} (the
+//                  eight k-elements one lane feeds the PV matrix op), at unit
+//                  u ^ ((d >> 1) & 7) of row d
+// The XOR placements make the kernel's 16-byte operand reads of 16
+// consecutive lanes hit 16 distinct bank quads (64 banks), and the kernel
+// copies a tile with plain contiguous direct-to-LDS loads.
 //
 // The attention kernel then works in the transposed orientation, which fits
 // the MFMA register layouts without any transpose:
@@ -16,11 +28,15 @@
 //   softmax per query column (keys = C rows: 4 per lane, 4 lane groups)
 //   O^T[dim][query] += V^T . P^T  A = value rows (dimension-major tile),
 //                                B = P^T straight from the S^T accumulators
-// with qh.kh + qh.kl + ql.kh and vh.ph + vh.pl + vl.ph.  Each workgroup (4
-// waves x 32 query rows) streams 64-key tiles of one (sequence, query head,
-// key split) and writes the same (m, l, o) partials as the other attention
-// kernels; attn_combine_kernel merges splits and the history / recent parts.
+// with qh.kh + qh.kl + ql.kh and vh.ph + vh.pl + vl.ph.  Each workgroup (8
+// waves x 32 query rows) streams the 64-key tiles of one (sequence, query
+// head, key split), double-buffered: the next tile is copied straight into
+// LDS (global_load_lds_dwordx4) while the current one is computed.  It writes
+// the same (m, l, o) partials as the other attention kernels;
+// attn_combine_kernel merges splits and the history / recent parts.
 #include <math.h>
+
+#include <algorithm>
 
 #include "attention_internal.h"
 
@@ -34,11 +50,19 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kD = 128;
 constexpr int kKT = 64;           // keys per tile
 constexpr int kQW = 32;           // query rows per wave
-constexpr int kQB = 4 * kQW;      // query rows per workgroup
-constexpr int kKS = 136;          // halves per key row of the K tile (128 + 8 pad)
-constexpr int kVS = 72;           // halves per dim row of the V tile (64 + 8 pad)
+constexpr int kPW = 8;            // waves per workgroup
+constexpr int kPT = 64 * kPW;     // threads per workgroup
+constexpr int kQB = kPW * kQW;    // query rows per workgroup
+constexpr int kImg = 32768;       // halves per tile image (64 KB)
+constexpr int kImgKL = 8192, kImgVH = 16384, kImgVL = 24576;  // part offsets (halves)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazy = 8.0f;     // softmax reference max raised by > 2^8 only
+
+// halves offset of 16-byte unit u of key row r / value row d in a tile image part
+__device__ __forceinline__ int kimg_off(int r, int u) { return r * 128 + 8 * (u ^ (r & 15)); }
+__device__ __forceinline__ int vimg_off(int d, int u) { return d * 64 + 8 * (u ^ ((d >> 1) & 7)); }
+// key (0..63) held by element e (0..7) of value unit u (0..7)
+__device__ __forceinline__ int vunit_key(int u, int e) { return 32 * (u >> 2) + 4 * (u & 3) + (e & 3) + 16 * (e >> 2); }
 
 __device__ __forceinline__ uint32_t h16(_Float16 h) { return (uint32_t)__builtin_bit_cast(uint16_t, h); }
 
@@ -55,9 +79,46 @@ __device__ __forceinline__ int exponent_of(float x) {
 }
 
 // ------------------------------------------------------------ pre-pass ----
-// One block = 64 tokens of one (sequence, KV head): thread (token tid/4,
-// dims 32*(tid%4)..) decodes its keys and values; values go dimension-major
-// through LDS.
+// One block = one 64-token tile of one (sequence, KV head): thread (token
+// tid/4, dims 32*(tid%4)..) decodes its keys and values; values go
+// dimension-major through LDS.  Every store is one 16-byte unit.
+__device__ __forceinline__ uint4 pack8(const _Float16* h) {
+  uint4 r;
+  r.x = h16(h[0]) | (h16(h[1]) << 16);
+  r.y = h16(h[2]) | (h16(h[3]) << 16);
+  r.z = h16(h[4]) | (h16(h[5]) << 16);
+  r.w = h16(h[6]) | (h16(h[7]) << 16);
+  return r;
+}
+
+// keys of token tt (dims dq..dq+31) into the K parts; vs[d][tt] = values
+__device__ __forceinline__ void store_keys(_Float16* img, int tt, int dq, const float* kv) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    _Float16 hi[8], lo[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) split_f16(kv[8 * i + e], hi[e], lo[e]);
+    const int off = kimg_off(tt, dq / 8 + i);
+    *(uint4*)(img + off) = pack8(hi);
+    *(uint4*)(img + kImgKL + off) = pack8(lo);
+  }
+}
+
+// value rows: thread (dim tid/2, key half tid%2) writes units 4*(tid%2)..+3
+__device__ __forceinline__ void store_values(_Float16* img, const float (*vs)[kKT + 1], int tid) {
+  const int d = tid >> 1, st = tid & 1;
+#pragma unroll
+  for (int kg = 0; kg < 4; ++kg) {
+    const int u = 4 * st + kg;
+    _Float16 hi[8], lo[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) split_f16(vs[d][vunit_key(u, e)], hi[e], lo[e]);
+    const int off = vimg_off(d, u);
+    *(uint4*)(img + kImgVH + off) = pack8(hi);
+    *(uint4*)(img + kImgVL + off) = pack8(lo);
+  }
+}
+
 template <int KEY, typename TN, typename TV>
 __global__ __launch_bounds__(256) void decode_hist_planes_kernel(smaq_attn_params p, HistAddr addr,
                                                                  PrefillPlanes pl) {
@@ -68,9 +129,8 @@ __global__ __launch_bounds__(256) void decode_hist_planes_kernel(smaq_attn_param
   const int tt = tid >> 2, dq = 32 * (tid & 3);
   const int64_t t = t0 + tt;
   const int64_t len = p.hist_len ? min((int64_t)p.hist_len[b], (int64_t)p.max_hist_len) : p.max_hist_len;
-  const int64_t plane = ((int64_t)b * p.n_kv_heads + h) * pl.Lp;
-  _Float16* kh = pl.kh + (plane + t) * kD + dq;
-  _Float16* kl = pl.kl + (plane + t) * kD + dq;
+  _Float16* img = pl.img + (((int64_t)b * p.n_kv_heads + h) * (pl.Lp / kKT) + blockIdx.x) * kImg;
+  float kv[32];
   if (t < len) {
     const int64_t ra = addr.row(b, h, t);
     const uint8_t* kr = (const uint8_t*)p.key_bytes + ra * p.key_row_bytes;
@@ -78,21 +138,17 @@ __global__ __launch_bounds__(256) void decode_hist_planes_kernel(smaq_attn_param
     if (KEY == SMAQ_KEY_SCALAR) nrm = Num<TN>::to_f(((const TN*)p.key_norms)[ra]);
     const int kbits = p.key_bits, kvpb = (8 / kbits) > 1 ? 8 / kbits : 1;
     const uint32_t kmask = (1u << kbits) - 1u;
+#pragma unroll
     for (int i = 0; i < 32; ++i) {
       const int d = dq + i;
-      float kv;
       if (KEY == SMAQ_KEY_SCALAR) {
         const uint32_t byte = kr[d / kvpb];
-        kv = p.key_lut[(byte >> ((d % kvpb) * kbits)) & kmask] * nrm;
+        kv[i] = p.key_lut[(byte >> ((d % kvpb) * kbits)) & kmask] * nrm;
       } else {
         const int bd = p.vq_block_dim, nc = p.vq_centroids, blk = d / bd;
         const int ci = min((int)kr[blk], nc - 1);
-        kv = p.key_lut[((int64_t)blk * nc + ci) * bd + (d - blk * bd)];
+        kv[i] = p.key_lut[((int64_t)blk * nc + ci) * bd + (d - blk * bd)];
       }
-      _Float16 hi, lo;
-      split_f16(kv, hi, lo);
-      kh[i] = hi;
-      kl[i] = lo;
     }
     const uint8_t* vr = (const uint8_t*)p.val_bytes + ra * p.val_row_bytes;
     const int vbits = p.val_bits, vvpb = vbits == 2 ? 4 : (vbits == 4 ? 2 : 1);
@@ -108,26 +164,18 @@ __global__ __launch_bounds__(256) void decode_hist_planes_kernel(smaq_attn_param
       vs[d][tt] = (float)code * Num<TV>::to_f(vsc[gi]) + Num<TV>::to_f(vz[gi]);
     }
   } else {
+#pragma unroll
     for (int i = 0; i < 32; ++i) {
-      kh[i] = (_Float16)0.0f;
-      kl[i] = (_Float16)0.0f;
+      kv[i] = 0.0f;
       vs[dq + i][tt] = 0.0f;
     }
   }
+  store_keys(img, tt, dq, kv);
   __syncthreads();
-  // values: thread (dim tid/2, tokens 32*(tid%2)..)
-  const int d = tid >> 1, tq = 32 * (tid & 1);
-  _Float16* vh = pl.vh + (((int64_t)b * p.n_kv_heads + h) * kD + d) * pl.Lp + t0 + tq;
-  _Float16* vl = pl.vl + (((int64_t)b * p.n_kv_heads + h) * kD + d) * pl.Lp + t0 + tq;
-  for (int i = 0; i < 32; ++i) {
-    _Float16 hi, lo;
-    split_f16(vs[d][tq + i], hi, lo);
-    vh[i] = hi;
-    vl[i] = lo;
-  }
+  store_values(img, vs, tid);
 }
 
-// Recent window: recent_k/v [batch][R][Hkv][D] -> planes.
+// Recent window: recent_k/v [batch][R][Hkv][D] -> tile images.
 template <typename TR>
 __global__ __launch_bounds__(256) void decode_recent_planes_kernel(smaq_attn_params p, PrefillPlanes pl) {
   __shared__ float vs[kD][kKT + 1];
@@ -137,41 +185,30 @@ __global__ __launch_bounds__(256) void decode_recent_planes_kernel(smaq_attn_par
   const int tt = tid >> 2, dq = 32 * (tid & 3);
   const int64_t t = t0 + tt;
   const int64_t len = p.recent_len ? min((int64_t)p.recent_len[b], (int64_t)p.max_recent_len) : p.max_recent_len;
-  const int64_t plane = ((int64_t)b * p.n_kv_heads + h) * pl.Lp;
-  _Float16* kh = pl.kh + (plane + t) * kD + dq;
-  _Float16* kl = pl.kl + (plane + t) * kD + dq;
+  _Float16* img = pl.img + (((int64_t)b * p.n_kv_heads + h) * (pl.Lp / kKT) + blockIdx.x) * kImg;
   const int64_t src = (int64_t)b * p.recent_batch_stride + (t * p.n_kv_heads + h) * kD + dq;
+  float kv[32];
+#pragma unroll
   for (int i = 0; i < 32; ++i) {
-    float kv = 0.0f, vv = 0.0f;
+    float vv = 0.0f;
+    kv[i] = 0.0f;
     if (t < len) {
-      kv = Num<TR>::to_f(((const TR*)p.recent_k)[src + i]);
+      kv[i] = Num<TR>::to_f(((const TR*)p.recent_k)[src + i]);
       vv = Num<TR>::to_f(((const TR*)p.recent_v)[src + i]);
     }
-    _Float16 hi, lo;
-    split_f16(kv, hi, lo);
-    kh[i] = hi;
-    kl[i] = lo;
     vs[dq + i][tt] = vv;
   }
+  store_keys(img, tt, dq, kv);
   __syncthreads();
-  const int d = tid >> 1, tq = 32 * (tid & 1);
-  _Float16* vh = pl.vh + (((int64_t)b * p.n_kv_heads + h) * kD + d) * pl.Lp + t0 + tq;
-  _Float16* vl = pl.vl + (((int64_t)b * p.n_kv_heads + h) * kD + d) * pl.Lp + t0 + tq;
-  for (int i = 0; i < 32; ++i) {
-    _Float16 hi, lo;
-    split_f16(vs[d][tq + i], hi, lo);
-    vh[i] = hi;
-    vl[i] = lo;
-  }
+  store_values(img, vs, tid);
 }
 
 // --------------------------------------------------------------- kernel ----
 // grid: x = key split, y = query head, z = sequence * query blocks
 template <bool CAUSAL>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_mfma_kernel(
+__global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_mfma_kernel(
     smaq_attn_params p, PrefillPart pp, Partials part) {
-  __shared__ __attribute__((aligned(16))) _Float16 ktile[2][kKT * kKS];   // [hi/lo][key][dim]
-  __shared__ __attribute__((aligned(16))) _Float16 vtile[2][kD * kVS];    // [hi/lo][dim][key]
+  __shared__ __attribute__((aligned(16))) _Float16 tiles[2][kImg];   // double-buffered tile images
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int n = lane & 15, kg = lane >> 4;
@@ -251,31 +288,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
     for (int db = 0; db < 8; ++db) acc_o[qb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int64_t plane = ((int64_t)b * p.n_kv_heads + h) * pp.Lp;
-  for (int64_t kt0 = k0; kt0 < k1; kt0 += kKT) {
-    // ---- stage the 64-key tile: K rows [key][dim], V rows [dim][key]
-    __syncthreads();
-    {
-      // K: 64 keys x 256 B per part = 1024 x 16 B pieces per part
+  // ---- tile images of this (sequence, KV head); tile kt0 / 64 is copied into
+  // tiles[i & 1] by direct-to-LDS loads: 4096 16-byte units, 8 per thread;
+  // load j of wave w covers units 512 j + 64 w .. + 63, contiguous in LDS
+  const _Float16* img0 = pp.img + ((int64_t)b * p.n_kv_heads + h) * (pp.Lp / kKT) * kImg;
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+  auto copy_tile = [&](int64_t kt, int buf) {
+    const _Float16* src = img0 + (kt / kKT) * kImg;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int piece = tid + 256 * i;          // 0..1023
-        const int key = piece >> 4, c = piece & 15;
-        const int64_t gi = (plane + kt0 + key) * kD + 8 * c;
-        *(uint4*)&ktile[0][key * kKS + 8 * c] = *(const uint4*)(pp.kh + gi);
-        *(uint4*)&ktile[1][key * kKS + 8 * c] = *(const uint4*)(pp.kl + gi);
-      }
-      // V: 128 dims x 128 B per part = 1024 x 16 B pieces per part
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int piece = tid + 256 * i;
-        const int d = piece >> 3, c = piece & 7;
-        const int64_t gi = (((int64_t)b * p.n_kv_heads + h) * kD + d) * pp.Lp + kt0 + 8 * c;
-        *(uint4*)&vtile[0][d * kVS + 8 * c] = *(const uint4*)(pp.vh + gi);
-        *(uint4*)&vtile[1][d * kVS + 8 * c] = *(const uint4*)(pp.vl + gi);
-      }
+    for (int j = 0; j < kImg * 2 / 16 / kPT; ++j) {
+      const int unit0 = kPT * j + 64 * wu;
+      __builtin_amdgcn_global_load_lds((const void*)(src + 8 * (unit0 + lane)),
+                                       (__attribute__((address_space(3))) void*)(&tiles[buf][8 * unit0]), 16, 0, 0);
     }
+  };
+  if (k0 < k1) copy_tile(k0, 0);
+  int it = 0;
+  for (int64_t kt0 = k0; kt0 < k1; kt0 += kKT, ++it) {
+    // this tile's copy has landed for every thread, and every wave is done
+    // with the other buffer, which then takes the next tile
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    if (kt0 + kKT < k1) copy_tile(kt0 + kKT, (it + 1) & 1);
+    const _Float16* kimg = tiles[it & 1];
+    const _Float16* vimg = tiles[it & 1] + kImgVH;
     // ---- S^T = K Q^T: keys 16kb + 4kg + v (rows), query 16qb + n (column)
     f32x4 sacc[2][4];
 #pragma unroll
@@ -286,9 +322,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        const int off = (16 * kb + n) * kKS + 32 * ks + 8 * kg;
-        const u32x4 ah = *(const u32x4*)&ktile[0][off];
-        const u32x4 al = *(const u32x4*)&ktile[1][off];
+        // key row 16 kb + n, dims 32 ks + 8 kg .. + 7 (unit 4 ks + kg)
+        const int off = kimg_off(16 * kb + n, 4 * ks + kg);
+        const u32x4 ah = *(const u32x4*)&kimg[off];
+        const u32x4 al = *(const u32x4*)&kimg[kImgKL + off];
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) {
           sacc[qb][kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, ah),
@@ -358,11 +395,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
       for (int db = 0; db < 8; ++db) {
         // A: dim 16db + n, keys 32st + 4kg + 0..3 and 32st + 16 + 4kg + 0..3
-        const int base = (16 * db + n) * kVS + 32 * st + 4 * kg;
-        const uint2 h0 = *(const uint2*)&vtile[0][base], h1 = *(const uint2*)&vtile[0][base + 16];
-        const uint2 l0 = *(const uint2*)&vtile[1][base], l1 = *(const uint2*)&vtile[1][base + 16];
-        const u32x4 avh = u32x4{h0.x, h0.y, h1.x, h1.y};
-        const u32x4 avl = u32x4{l0.x, l0.y, l1.x, l1.y};
+        // (one unit of the value image)
+        const int off = vimg_off(16 * db + n, 4 * st + kg);
+        const u32x4 avh = *(const u32x4*)&vimg[off];
+        const u32x4 avl = *(const u32x4*)&vimg[kImgVL - kImgVH + off];
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) {
           acc_o[qb][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, avh),
@@ -410,10 +446,34 @@ bool prefill_mfma_supported(const smaq_attn_params& p) {
 
 int64_t prefill_padded_len(int64_t L) { return ((L + kKT - 1) / kKT) * kKT; }
 
+// Workgroups hold 128 KB of LDS, one per CU.  Split the keys so that the
+// grid covers at least three rounds of the device's CUs and, among up to
+// twice that many splits, the one whose last round is fullest (splits of at
+// least four tiles).
 int64_t prefill_split_len(const smaq_attn_params& p, int64_t L) {
+  static int n_cu = 0;
+  if (n_cu <= 0) {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
+      n_cu = cus;
+    else
+      n_cu = 256;
+  }
   const int64_t wgs = (int64_t)p.batch * p.n_q_heads * ((p.q_len + kQB - 1) / kQB);
-  const int64_t want = wgs >= 512 ? 1 : (512 + wgs - 1) / wgs;
-  int64_t split = (L + want - 1) / want;
+  const int64_t max_s = (L + 4 * kKT - 1) / (4 * kKT);
+  const int64_t s_min = std::min(max_s, std::max<int64_t>(1, (3 * n_cu + wgs - 1) / wgs));
+  int64_t best = s_min;
+  double best_fill = -1.0;
+  for (int64_t s = s_min; s <= std::min(max_s, 2 * s_min); ++s) {
+    const int64_t n = wgs * s, rounds = (n + n_cu - 1) / n_cu;
+    const double fill = (double)n / ((double)n_cu * (double)rounds);
+    if (fill > best_fill + 1e-9) {
+      best_fill = fill;
+      best = s;
+    }
+  }
+  int64_t split = (L + best - 1) / best;
   split = ((split + kKT - 1) / kKT) * kKT;
   return split < 4 * kKT ? 4 * kKT : split;
 }
@@ -455,9 +515,9 @@ int launch_prefill_mfma(const smaq_attn_params& p, const PrefillPart& pp, int n_
   const int nqb = (p.q_len + kQB - 1) / kQB;
   dim3 grid((unsigned)n_splits, p.n_q_heads, (unsigned)(p.batch * nqb));
   if (p.q_positions)
-    hipLaunchKernelGGL(prefill_mfma_kernel<true>, grid, dim3(256), 0, st, p, pp, part);
+    hipLaunchKernelGGL(prefill_mfma_kernel<true>, grid, dim3(kPT), 0, st, p, pp, part);
   else
-    hipLaunchKernelGGL(prefill_mfma_kernel<false>, grid, dim3(256), 0, st, p, pp, part);
+    hipLaunchKernelGGL(prefill_mfma_kernel<false>, grid, dim3(kPT), 0, st, p, pp, part);
   return launch_status("smaq_attn_hybrid(prefill)");
 }
 

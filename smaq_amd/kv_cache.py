@@ -152,7 +152,8 @@ class SMAQKVCache:
             else:
                 parts.append(self.key_quantizer.attention_score(query, self.key_quantized, scale=scale))
         if self.key_buffer is not None:
-            parts.append(torch.matmul(query, self.key_buffer.transpose(-2, -1)) * scale)
+            # (a contiguous right operand: batched bf16 products of a transposed view are avoided)
+            parts.append(torch.matmul(query, self.key_buffer.transpose(-2, -1).contiguous()) * scale)
         if not parts:
             return torch.empty(*query.shape[:-2], query.shape[-2], 0, device=query.device, dtype=query.dtype)
         return torch.cat(parts, dim=-1)

@@ -120,6 +120,38 @@ int smaq_dequant_blockvq(const void* idx, long long rows, int n_blocks, int bloc
                          int n_centroids, const float* decoded, float* out, void* stream);
 
 /*
+ * Block-VQ calibration on the device.  The reference fits its codebook with
+ * torch ops on the calibration data's device (smaq/block_vq.py:37-79 _kmeans,
+ * :190-203 fit); these three steps are that fit's arithmetic, with the
+ * assignment step done by smaq_encode_blockvq:
+ *
+ * smaq_blockvq_shape replaces `calibration_keys[:, bj].float() @ E.T`
+ * (smaq/block_vq.py:196) for every block: x[b][r][i] = sum_d k[r][b*bd+d] *
+ * E_b[i][d] (sequential FMA over d, the encoder's own shaped keys).
+ *   k [rows][n_blocks*block_dim] contiguous; x_out [n_blocks][rows][block_dim] fp32.
+ */
+int smaq_blockvq_shape(const void* k, int kdtype, long long rows, int n_blocks, int block_dim,
+                       const float* E_blocks, float* x_out, void* stream);
+
+/*
+ * k-means++ seeding distances (smaq/block_vq.py:54-61, the squared distance
+ * of every point to its nearest chosen centroid): dmin[b][r] =
+ * |x[b][r] - x[b][pick[b]]|^2 when `first`, else the minimum of that and
+ * dmin[b][r].  pick: [n_blocks] row indices (device int64).
+ */
+int smaq_kmeanspp_update(const float* x, int n_blocks, long long rows, int block_dim,
+                         const long long* pick, int first, float* dmin, void* stream);
+
+/*
+ * Lloyd centroid update (smaq/block_vq.py:70-77): centroid (b, j) = mean of
+ * the x[b][r] with idx[r][b] == j; centroids with no rows keep their value.
+ * idx [rows][n_blocks] uint8 (smaq_encode_blockvq's output); centroids
+ * [n_blocks][n_centroids][block_dim] fp32, updated in place.  Deterministic.
+ */
+int smaq_kmeans_update(const float* x, const unsigned char* idx, int n_blocks, long long rows,
+                       int block_dim, int n_centroids, float* centroids, void* stream);
+
+/*
  * Fused quantized-KV attention (decode and prefill).  Replaces
  * compute_hybrid_attention (smaq/score.py:23-72) with its per-head score loop
  * (smaq/score.py:75-96), value dequantisation (smaq/kv_cache.py:94-103) and

@@ -75,6 +75,9 @@ _SIGS = {
                                     c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "smaq_dequant_blockvq": (c_int, [c_void_p, c_ll, c_int, c_int, c_int, c_void_p, c_void_p,
                                      c_void_p]),
+    "smaq_blockvq_shape": (c_int, [c_void_p, c_int, c_ll, c_int, c_int, c_void_p, c_void_p, c_void_p]),
+    "smaq_kmeanspp_update": (c_int, [c_void_p, c_int, c_ll, c_int, c_void_p, c_int, c_void_p, c_void_p]),
+    "smaq_kmeans_update": (c_int, [c_void_p, c_void_p, c_int, c_ll, c_int, c_int, c_void_p, c_void_p]),
     "smaq_attn_workspace_bytes": (c_ll, [ctypes.POINTER(AttnParams)]),
     "smaq_attn_hybrid": (c_int, [ctypes.POINTER(AttnParams), c_void_p]),
 }
@@ -321,6 +324,46 @@ def encode_blockvq(k: torch.Tensor, E_blocks: torch.Tensor, centroids: torch.Ten
                                      _ptr(cents), _ptr(idx), ties.ptr() if ties else None, _stream(dev)),
            "smaq_encode_blockvq")
     return idx
+
+
+def blockvq_shape(k: torch.Tensor, E_blocks: torch.Tensor) -> torch.Tensor:
+    """Shaped calibration keys: k [N, nb * bd] -> x [nb, N, bd] fp32 (x = k_b E_b^T)."""
+    dev = require_gpu(k, E_blocks)
+    nb, bd, _ = E_blocks.shape
+    if k.dim() != 2 or k.shape[1] != nb * bd:
+        raise ValueError(f"keys must be [N, {nb * bd}], got {tuple(k.shape)}")
+    kc = k.contiguous()
+    eb = E_blocks.to(torch.float32).contiguous()
+    x = torch.empty(nb, k.shape[0], bd, dtype=torch.float32, device=dev)
+    _check(lib().smaq_blockvq_shape(_ptr(kc), dtype_code(kc.dtype), kc.shape[0], nb, bd, _ptr(eb), _ptr(x),
+                                    _stream(dev)), "smaq_blockvq_shape")
+    return x
+
+
+def kmeanspp_update(x: torch.Tensor, pick: torch.Tensor, dmin: torch.Tensor, first: bool) -> None:
+    """dmin [nb, N] <- (first ? d : min(dmin, d)), d = squared distance to x[b][pick[b]]."""
+    dev = require_gpu(x, pick, dmin)
+    nb, n, bd = x.shape
+    if pick.shape != (nb,) or dmin.shape != (nb, n) or dmin.dtype != torch.float32 or not dmin.is_contiguous():
+        raise ValueError("kmeanspp_update: pick must be [n_blocks], dmin a contiguous fp32 [n_blocks, N]")
+    pk = pick.to(torch.int64).contiguous()
+    xc = x.contiguous()
+    _check(lib().smaq_kmeanspp_update(_ptr(xc), nb, n, bd, _ptr(pk), 1 if first else 0, _ptr(dmin), _stream(dev)),
+           "smaq_kmeanspp_update")
+
+
+def kmeans_update(x: torch.Tensor, idx: torch.Tensor, centroids: torch.Tensor) -> None:
+    """centroids [nb, nc, bd] <- per-cluster means of x [nb, N, bd] under idx [N, nb] (in place)."""
+    dev = require_gpu(x, idx, centroids)
+    nb, n, bd = x.shape
+    nc = centroids.shape[1]
+    if (idx.shape != (n, nb) or idx.dtype != torch.uint8 or centroids.shape != (nb, nc, bd)
+            or centroids.dtype != torch.float32 or not centroids.is_contiguous()):
+        raise ValueError("kmeans_update: idx must be uint8 [N, n_blocks], centroids contiguous fp32 "
+                         "[n_blocks, n_centroids, block_dim]")
+    xc, ic = x.contiguous(), idx.contiguous()
+    _check(lib().smaq_kmeans_update(_ptr(xc), _ptr(ic), nb, n, bd, nc, _ptr(centroids), _stream(dev)),
+           "smaq_kmeans_update")
 
 
 def dequant_blockvq(idx: torch.Tensor, decoded: torch.Tensor) -> torch.Tensor:

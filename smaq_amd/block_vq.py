@@ -3,8 +3,9 @@
 Keys are cut into ``block_dim``-dim blocks; each block is mapped by its own
 metric ``E_b`` and replaced by the index of the nearest of ``n_centroids``
 codewords; decoding is a table lookup of pre-decoded centroids.  Calibration
-(``fit``: per-block metric + k-means++/Lloyd) runs on the host CPU with torch;
-``quantize`` and ``dequantize`` are HIP kernels.
+(``fit``: per-block metric + k-means++/Lloyd) runs on the host CPU with torch
+(the reference's codebook for a seed), or with ``on_device=True`` on the GPU
+through HIP kernels; ``quantize`` and ``dequantize`` are HIP kernels.
 
 Indices are stored as uint8 (n_centroids <= 256) rather than the reference's
 int64: the values are identical (decoders call ``.long()``), the cache is 8x
@@ -100,17 +101,30 @@ class SMAQBlockVQ(nn.Module):
         return math.log2(self.n_centroids) / self.block_dim
 
     def fit(self, calibration_keys: torch.Tensor, calibration_queries: torch.Tensor, kmeans_iters: int = 20,
-            seed: int = 42) -> "SMAQBlockVQ":
+            seed: int = 42, on_device: bool = False) -> "SMAQBlockVQ":
         """Per block: uncentred Sigma_q, metric, k-means in the shaped space,
-        pre-decoded centroids (smaq/block_vq.py:160-210).  Host CPU, fp32."""
-        keys = calibration_keys.detach().to("cpu")
+        pre-decoded centroids (smaq/block_vq.py:160-210).
+
+        Host CPU, fp32, by default: the codebook is the reference's for the
+        same seed.  ``on_device=True`` (an extension) runs the k-means on the
+        quantizer's GPU with the HIP kernels (all blocks at once, incremental
+        k-means++ distances, the encoder as the assignment step); the device
+        random stream differs from the CPU one, so that codebook is a
+        different draw of the same algorithm (compare with ``logit_mse``)."""
         queries = calibration_queries.detach().to("cpu")
-        n = keys.shape[0]
-        Es, Eis, Cs, Ds = [], [], [], []
+        n = queries.shape[0]
+        metrics = []
         for bi in range(self.n_blocks):
             sl = slice(bi * self.block_dim, (bi + 1) * self.block_dim)
             qb = queries[:, sl].float()
-            E, E_inv = build_smaq_metric((qb.T @ qb) / n, c=self.c)
+            metrics.append(build_smaq_metric((qb.T @ qb) / n, c=self.c))
+        if on_device:
+            return self._fit_on_device(calibration_keys, metrics, kmeans_iters, seed)
+        keys = calibration_keys.detach().to("cpu")
+        Es, Eis, Cs, Ds = [], [], [], []
+        for bi in range(self.n_blocks):
+            sl = slice(bi * self.block_dim, (bi + 1) * self.block_dim)
+            E, E_inv = metrics[bi]
             cents = _kmeans(keys[:, sl].float() @ E.T, self.n_centroids, kmeans_iters, seed + bi)
             Es.append(E)
             Eis.append(E_inv)
@@ -120,6 +134,45 @@ class SMAQBlockVQ(nn.Module):
         self.E_inv_blocks = torch.stack(Eis).to(self._device, self._dtype)
         self.centroids = torch.stack(Cs).to(self._device, self._dtype)
         self.decoded_centroids = torch.stack(Ds).to(self._device, self._dtype)
+        self._fitted = True
+        return self
+
+    def _fit_on_device(self, calibration_keys, metrics, kmeans_iters: int, seed: int) -> "SMAQBlockVQ":
+        dev = self._device
+        keys = calibration_keys.detach().to(dev)
+        if keys.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+            keys = keys.float()
+        keys = keys.contiguous()
+        n, nb, bd, nc = keys.shape[0], self.n_blocks, self.block_dim, self.n_centroids
+        E_blocks = torch.stack([m[0] for m in metrics]).to(dev, torch.float32)
+        E_inv_blocks = torch.stack([m[1] for m in metrics]).to(dev, torch.float32)
+        x = _native.blockvq_shape(keys, E_blocks)                   # [nb, n, bd]
+        if n <= nc:
+            cents = torch.zeros(nb, nc, bd, dtype=torch.float32, device=dev)
+            cents[:, :n] = x
+        else:
+            gen = torch.Generator(device=dev).manual_seed(seed)
+            pick = torch.randint(n, (nb,), generator=gen, device=dev)
+            picks = [pick]
+            dmin = torch.empty(nb, n, dtype=torch.float32, device=dev)
+            _native.kmeanspp_update(x, pick, dmin, first=True)
+            for _ in range(nc - 1):
+                # draw with probability proportional to the squared distance to
+                # the nearest pick; a block whose points all coincide with
+                # picks draws uniformly (smaq/block_vq.py:56-61)
+                w = torch.where(dmin.sum(dim=1, keepdim=True) > 0, dmin, torch.ones_like(dmin))
+                pick = torch.multinomial(w, 1, generator=gen).squeeze(1)
+                picks.append(pick)
+                _native.kmeanspp_update(x, pick, dmin, first=False)
+            sel = torch.stack(picks, dim=1)                          # [nb, nc]
+            cents = torch.gather(x, 1, sel.unsqueeze(-1).expand(nb, nc, bd)).contiguous()
+            for _ in range(kmeans_iters):
+                idx = _native.encode_blockvq(keys, E_blocks, cents)   # [n, nb]
+                _native.kmeans_update(x, idx, cents)
+        self.E_blocks = E_blocks.to(self._dtype)
+        self.E_inv_blocks = E_inv_blocks.to(self._dtype)
+        self.centroids = cents.to(self._dtype)
+        self.decoded_centroids = torch.bmm(cents, E_inv_blocks.transpose(1, 2).contiguous()).to(self._dtype)
         self._fitted = True
         return self
 

@@ -6,23 +6,32 @@
 //   x_e  = sequential fmaf chain over d of k_d * E_b[e][d]
 //   d2_c = fmaf chain over e of (-2 x_e) * C_c[e], + |x|^2, + |C_c|^2,
 //          clamp_min(0); index = first minimum of sqrt(d2)  (cdist's matmul form)
-// Here x is computed the same way (bit for bit), and all 256 distances of a
-// (token, block) come from three v_mfma_f32_16x16x4_f32 per 16 centroids:
-// A = [C_c[0..3]], [C_c[4..7]], [|C_c|^2, 1, 0, 0], B = [-2x[0..3]],
-// [-2x[4..7]], [1, |x|^2 + delta, 0, 0].  Those values differ from the
-// reference's chain only by rounding order, at most 3e-6 * (|x|^2 + max |C|^2)
-// for these 12-term sums, so the argmin is the reference's whenever the
-// runner-up is more than delta = 1.2e-5 * (|x|^2 + max |C|^2) behind the best.
-// Otherwise (about 1e-3 of the (token, block) pairs on SMAQ-shaped keys, or a
-// non-finite key) the whole wave recomputes that pair's 256 distances with
-// the exact chain and takes the reference's argmin and tie count.
+// Here x is computed the same way (bit for bit).  The 256 distances of a
+// (token, block) come from one v_mfma_f32_16x16x32_f16 per 16 centroids, on
+// a power-of-two rescaling of the block (sigma_b puts the largest centroid
+// component in [2^11, 2^12), far above the f16 subnormal range):
+//   y = -2 sigma x split as yh + yl (f16), sigma C split as ch + cl (f16),
+//   K slots  [ch . yh | ch . yl | cl . yh | (q_hi, q_lo) . 2^14]
+//   with q = |sigma C|^2 / 2^14 split hi/lo, and the accumulator starting at
+//   sigma^2 (|x|^2 + delta).
+// The dropped cl . yl term and the f16 splits cost at most ~1e-6 of
+// S = |x|^2 + max |C|^2 (4.5e-7 on SMAQ-shaped keys against the reference's
+// distances), the fp32 sums of 27 terms at most 27 ulps of S (1.6e-6), the
+// reference's own rounding ~1.5e-6: each distance is within 4e-6 S of the
+// reference's, so the argmin is the reference's whenever the runner-up is more
+// than delta = 1.2e-5 S behind the best.  Otherwise (about 1e-3 of the
+// (token, block) pairs on SMAQ-shaped keys; a key component beyond
+// 2^13 / sigma; a non-finite key) the whole wave recomputes that pair's 256
+// distances with the exact chain from the fp32 codebook in global memory and
+// takes the reference's argmin and tie count.
 //
-// Layout: one persistent workgroup of 16 waves per CU holds the codebook in
-// LDS in MFMA A-operand order (8 KB per block, conflict-free dword reads) plus
-// |C|^2 and E; each wave encodes 16 tokens at a time, block after block.  The
-// running minimum keeps the distance bits with the low 6 bits replaced by the
-// centroid's position in the lane (tile, row), so one v_min_u32 tracks value
-// and index (distances are positive: delta is added to every one).
+// Layout: one persistent workgroup of 16 waves per CU holds the split
+// codebook in LDS (16-byte rows, conflict-free ds_read_b128); each wave
+// encodes 16 tokens at a time, block after block, with the next block's key
+// bytes in flight.  The running minimum keeps the distance bits with the low
+// 6 bits replaced by the centroid's position in the lane (tile, row), so one
+// v_min_u32 tracks value and index (distances are positive: delta is added to
+// every one) and one v_med3_u32 the runner-up.
 #include "encode_internal.h"
 
 namespace smaq {
@@ -30,57 +39,101 @@ namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kVmWaves = 16;                  // waves per workgroup (4 per SIMD)
 constexpr int kVmThreads = 64 * kVmWaves;
 constexpr int kVmNc = 256;                    // centroids per block
 constexpr int kVmBd = 8;                      // block dim
 constexpr int kVmMaxBlocks = 16;
-constexpr int kCtBlock = 2 * 2 * kVmNc * 2;   // floats of one block's A operands
 constexpr float kDeltaRel = 1.2e-5f;
+constexpr float kYMax = 16384.0f;             // |y| bound (f16 operands, their hi parts rounded)
+constexpr float kQScale = 16384.0f;           // 2^14: |sigma C|^2 is stored divided by this
+
+// LDS map (bytes) for nb blocks
+struct VmLds {
+  int nb;
+  __host__ __device__ int nq() const { return (nb + 3) / 4; }
+  __host__ __device__ size_t ch() const { return 0; }                                  // [nb][256] x 16 B
+  __host__ __device__ size_t cl() const { return (size_t)nb * kVmNc * 16; }            // [nb][256] x 16 B
+  __host__ __device__ size_t cq() const { return 2 * (size_t)nb * kVmNc * 16; }        // [nq][256] x 16 B
+  __host__ __device__ size_t bq() const { return cq() + (size_t)nq() * kVmNc * 16; }   // [4] x 16 B
+  __host__ __device__ size_t ys() const { return bq() + 64; }                          // [16 waves][16] x 32 B
+  __host__ __device__ size_t es() const { return ys() + (size_t)kVmWaves * 16 * 32; }  // [nb][64] f32
+  __host__ __device__ size_t sig() const { return es() + (size_t)nb * 64 * 4; }        // [nb] f32
+  __host__ __device__ size_t smax() const { return sig() + (size_t)nb * 4; }           // [nb] f32
+  __host__ __device__ size_t bytes() const { return smax() + (size_t)nb * 4; }
+};
 
 __device__ __forceinline__ uint32_t fbits(float x) { return __builtin_bit_cast(uint32_t, x); }
 __device__ __forceinline__ float bitsf(uint32_t b) { return __builtin_bit_cast(float, b); }
+__device__ __forceinline__ uint32_t h16(_Float16 h) { return (uint32_t)__builtin_bit_cast(uint16_t, h); }
 
-template <typename T>
-__device__ __forceinline__ void load8(const T* p, float* out) {
-  if constexpr (sizeof(T) == 2) {
-    const u32x4 v = *(const u32x4*)p;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      out[2 * i] = Num<T>::to_f(__builtin_bit_cast(T, (uint16_t)v[i]));
-      out[2 * i + 1] = Num<T>::to_f(__builtin_bit_cast(T, (uint16_t)(v[i] >> 16)));
-    }
-  } else {
-    const u32x4 a = *(const u32x4*)p, b = *(const u32x4*)(p + 4);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      out[i] = bitsf(a[i]);
-      out[4 + i] = bitsf(b[i]);
-    }
-  }
+// Middle of three (v_med3_u32): with best <= second, med3(best, second, key)
+// is the new runner-up after `key`.
+__device__ __forceinline__ uint32_t med3_u32(uint32_t a, uint32_t b, uint32_t c) {
+  uint32_t r;
+  asm("v_med3_u32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
 }
 
+// Orders this wave's LDS writes before its later LDS reads of other lanes'
+// data (a wave-local exchange).
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// One token's 8-value key block, kept as loaded (16 or 32 bytes).
+template <typename T>
+struct KeyBlock {
+  static constexpr int kWords = sizeof(T) == 2 ? 4 : 8;
+  u32x4 w[kWords / 4];
+  __device__ __forceinline__ void load(const T* p) {
+    w[0] = *(const u32x4*)p;
+    if constexpr (sizeof(T) == 4) w[1] = *(const u32x4*)(p + 4);
+  }
+  __device__ __forceinline__ void unpack(float* out) const {
+    if constexpr (sizeof(T) == 2) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        out[2 * i] = Num<T>::to_f(__builtin_bit_cast(T, (uint16_t)w[0][i]));
+        out[2 * i + 1] = Num<T>::to_f(__builtin_bit_cast(T, (uint16_t)(w[0][i] >> 16)));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        out[i] = bitsf(w[0][i]);
+        out[4 + i] = bitsf(w[1][i]);
+      }
+    }
+  }
+};
+
 // Exact distances of one (token, block) by the whole wave (4 centroids per
-// lane) and the reference's choice: first index of the smallest sqrt(d2),
-// with NaN winning at its first index; `tie` when another centroid is within
-// 2e-6 relative of the smallest d2.
-__device__ int exact_argmin(const float* x, float xsq, const float* ct, const float* csq, int lane,
-                            bool* tie) {
+// lane, read from the fp32 codebook Cb = C[b] in global memory) and the
+// reference's choice: first index of the smallest sqrt(d2), with NaN winning
+// at its first index; `tie` when another centroid is within 2e-6 relative of
+// the smallest d2.
+__device__ int exact_argmin(const float* x, float xsq, const float* __restrict__ Cb, int lane, bool* tie) {
   uint64_t key = ~0ull;
   float dmin = __builtin_inff();
   float d2v[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int c = lane + 64 * j;
-    float a = 0.0f;
+    float ce[kVmBd];
+#pragma unroll
+    for (int e = 0; e < kVmBd; ++e) ce[e] = Cb[c * kVmBd + e];
+    float a = 0.0f, csq = 0.0f;
 #pragma unroll
     for (int e = 0; e < kVmBd; ++e) {
-      const float ce = ct[((e >> 2) * 2 + ((e >> 1) & 1)) * (2 * kVmNc) + 2 * c + (e & 1)];
-      a = fmaf(-2.0f * x[e], ce, a);
+      a = fmaf(-2.0f * x[e], ce[e], a);
+      csq = csq + ce[e] * ce[e];  // x.pow(2).sum(-1) order
     }
     a = a + xsq;
-    a = a + csq[c];
+    a = a + csq;
     a = a < 0.0f ? 0.0f : a;  // clamp_min(0); NaN passes
     d2v[j] = a;
     const bool nan = a != a;
@@ -110,45 +163,102 @@ template <typename T>
 __global__ __launch_bounds__(kVmThreads) void encode_blockvq_mfma_kernel(
     const T* __restrict__ k, RowMap map, int64_t rows, int nb, const float* __restrict__ E_blocks,
     const float* __restrict__ C, uint8_t* __restrict__ idx_out, unsigned long long* tie_count) {
-  extern __shared__ float lds[];
-  float* const ct_all = lds;                          // [nb][2 steps][2 k-pairs][256][2]
-  float* const csq_all = ct_all + nb * kCtBlock;      // [nb][256]
-  float* const es_all = csq_all + nb * kVmNc;         // [nb][8][8]
-  float* const cmax_all = es_all + nb * 64;           // [nb] max |C|^2
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const VmLds L{nb};
+  float* const es_all = (float*)(lds + L.es());
+  float* const sig_all = (float*)(lds + L.sig());
+  float* const smax_all = (float*)(lds + L.smax());
   const int tid = threadIdx.x;
-  for (int i = tid; i < nb * kVmNc * kVmBd; i += kVmThreads) {
-    const int b = i / (kVmNc * kVmBd), r = i - b * (kVmNc * kVmBd);
-    const int c = r / kVmBd, e = r - c * kVmBd;
-    ct_all[b * kCtBlock + ((e >> 2) * 2 + ((e >> 1) & 1)) * (2 * kVmNc) + 2 * c + (e & 1)] = C[i];
-  }
-  for (int i = tid; i < nb * kVmNc; i += kVmThreads) {
-    const float* c = C + (int64_t)i * kVmBd;
-    float s = 0.0f;
-    for (int e = 0; e < kVmBd; ++e) s = s + c[e] * c[e];  // x.pow(2).sum(-1) order
-    csq_all[i] = s;
+  const int lane = tid & 63, w = tid >> 6;
+
+  // ---- per block: sigma_b (a power of two putting max |C| in [2^11, 2^12))
+  // and max |C|^2; one wave per block
+  for (int b = w; b < nb; b += kVmWaves) {
+    float amax = 0.0f, smax = 0.0f;
+    for (int c = lane; c < kVmNc; c += 64) {
+      const float* cc = C + ((int64_t)b * kVmNc + c) * kVmBd;
+      float s = 0.0f;
+      for (int e = 0; e < kVmBd; ++e) {
+        amax = fmaxf(amax, fabsf(cc[e]));
+        s = s + cc[e] * cc[e];
+      }
+      smax = fmaxf(smax, s);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+      smax = fmaxf(smax, __shfl_xor(smax, off, 64));
+    }
+    if (lane == 0) {
+      int e = 0;
+      if (amax > 0.0f && amax < 3.0e38f) frexpf(amax, &e);  // amax in [2^(e-1), 2^e)
+      // a codebook outside a sane range (or non-finite) sends every token to
+      // the exact path (NaN sigma makes every distance NaN)
+      sig_all[b] = (e > -100 && e < 100) ? ldexpf(1.0f, 12 - e) : __builtin_nanf("");
+      smax_all[b] = smax;
+    }
   }
   for (int i = tid; i < nb * 64; i += kVmThreads) es_all[i] = E_blocks[i];
+  if (tid < 16) {  // |C|^2 slot operands: row r holds 2^14 in halves 2r, 2r+1
+    const int r = tid >> 2, dw = tid & 3;
+    ((uint32_t*)(lds + L.bq()))[tid] = dw == r ? 0x74007400u : 0u;
+  }
   __syncthreads();
-  for (int b = tid; b < nb; b += kVmThreads) {
-    float m = 0.0f;
-    for (int c = 0; c < kVmNc; ++c) m = fmaxf(m, csq_all[b * kVmNc + c]);
-    cmax_all[b] = m;
+  // ---- split codebook: ch / cl rows of sigma C, q = |sigma C|^2 / 2^14 split
+  for (int i = tid; i < L.nq() * 4 * kVmNc; i += kVmThreads) {
+    const int c = i % kVmNc, jb = i / kVmNc;  // jb = 4 * (b / 4) + b % 4
+    const int b = jb;
+    uint32_t qw = 0u;
+    if (b < nb) {
+      const float sg = sig_all[b];
+      const float* cc = C + ((int64_t)b * kVmNc + c) * kVmBd;
+      uint32_t hw[4], lw[4];
+      float q = 0.0f;
+#pragma unroll
+      for (int e = 0; e < kVmBd; e += 2) {
+        const float v0 = cc[e] * sg, v1 = cc[e + 1] * sg;
+        const _Float16 h0 = (_Float16)v0, h1 = (_Float16)v1;
+        const _Float16 l0 = (_Float16)(v0 - (float)h0), l1 = (_Float16)(v1 - (float)h1);
+        hw[e >> 1] = h16(h0) | (h16(h1) << 16);
+        lw[e >> 1] = h16(l0) | (h16(l1) << 16);
+        q = fmaf(v0, v0, q);
+        q = fmaf(v1, v1, q);
+      }
+      *(u32x4*)(lds + L.ch() + ((size_t)b * kVmNc + c) * 16) = u32x4{hw[0], hw[1], hw[2], hw[3]};
+      *(u32x4*)(lds + L.cl() + ((size_t)b * kVmNc + c) * 16) = u32x4{lw[0], lw[1], lw[2], lw[3]};
+      const float qs = q * (1.0f / kQScale);
+      const _Float16 qh = (_Float16)qs, ql = (_Float16)(qs - (float)qh);
+      qw = sg == sg ? (h16(qh) | (h16(ql) << 16)) : 0u;
+    }
+    ((uint32_t*)(lds + L.cq()))[((size_t)(jb >> 2) * kVmNc + c) * 4 + (jb & 3)] = qw;
   }
   __syncthreads();
 
-  const int lane = tid & 63, w = tid >> 6;
   const int n = lane & 15, kg = lane >> 4;  // MFMA coordinates: token / centroid row n, k-group kg
-  typedef const __attribute__((address_space(3))) float LdsF;
+  uint8_t* const ys_w = lds + L.ys() + (size_t)w * 16 * 32;
+  _Float16* const ys_tok = (_Float16*)(ys_w + n * 32);  // this lane's token: y hi [8] | y lo [8]
   unsigned ties = 0;
   const int64_t n_tiles = (rows + 15) / 16;
-  for (int64_t tile = (int64_t)blockIdx.x * kVmWaves + w; tile < n_tiles;
-       tile += (int64_t)gridDim.x * kVmWaves) {
+  const int64_t stride = (int64_t)gridDim.x * kVmWaves;
+  int64_t tile = (int64_t)blockIdx.x * kVmWaves + w;
+  auto key_row = [&](int64_t t) -> const T* {
+    const int64_t row = t * 16 + n;
+    return k + map.offset(row < rows ? row : rows - 1);
+  };
+  // (key_row clamps past-the-end rows, so the prefetch past the last tile
+  // reads a valid row)
+  const T* kr = key_row(tile);
+  KeyBlock<T> next;
+  next.load(kr);
+  for (; tile < n_tiles; tile += stride) {
     const int64_t row = tile * 16 + n;
     const bool valid = row < rows;
-    const T* kr = k + map.offset(valid ? row : rows - 1);
+    const T* const kr_next = key_row(tile + stride);
     for (int b = 0; b < nb; ++b) {
       float kv[kVmBd];
-      load8<T>(kr + b * kVmBd, kv);
+      next.unpack(kv);
+      // the next key block of this lane's token (or the next tile's first)
+      next.load(b + 1 < nb ? kr + (b + 1) * kVmBd : kr_next);
       const float* es = es_all + b * 64;
       // x_kg and x_{kg+4}: the reference's chain, bit for bit
       float xa = 0.0f, xb = 0.0f;
@@ -157,30 +267,46 @@ __global__ __launch_bounds__(kVmThreads) void encode_blockvq_mfma_kernel(
         xa = fmaf(kv[d], es[kg * 8 + d], xa);
         xb = fmaf(kv[d], es[(kg + 4) * 8 + d], xb);
       }
-      float sq = xa * xa + xb * xb;
+      const float sg = sig_all[b];
+      const float ya = xa * (-2.0f * sg), yb = xb * (-2.0f * sg);  // exact (powers of two)
+      const bool ok = fabsf(ya) < kYMax && fabsf(yb) < kYMax;     // false for NaN
+      const _Float16 yah = (_Float16)ya, ybh = (_Float16)yb;
+      ys_tok[kg] = yah;
+      ys_tok[kg + 4] = ybh;
+      ys_tok[8 + kg] = (_Float16)(ya - (float)yah);
+      ys_tok[8 + kg + 4] = (_Float16)(yb - (float)ybh);
+      float sq = ok ? xa * xa + xb * xb : __builtin_nanf("");
       sq += __shfl_xor(sq, 16, 64);
       sq += __shfl_xor(sq, 32, 64);
-      const float delta = kDeltaRel * (sq + cmax_all[b]);
-      const float b0 = -2.0f * xa, b1 = -2.0f * xb;
-      const float b2 = kg == 0 ? 1.0f : (kg == 1 ? sq + delta : 0.0f);
-      const LdsF* ct = (const LdsF*)(ct_all + b * kCtBlock) + (kg >> 1) * (2 * kVmNc) + 2 * n + (kg & 1);
-      const LdsF* cs = (const LdsF*)(csq_all + b * kVmNc) + n;
+      const float delta = kDeltaRel * (sq + smax_all[b]);
+      const float s2 = sg * sg;
+      const float init = (sq + delta) * s2;  // |x|^2 + delta, scaled
+      const float delta_s = delta * s2;
+      wave_sync();
+      // B: k-group 0 / 2 take y hi, 1 takes y lo, 3 the 2^14 pair of block b
+      const uint8_t* bsrc = kg == 3 ? lds + L.bq() + (b & 3) * 16 : (const uint8_t*)ys_tok + (kg == 1 ? 16 : 0);
+      const f16x8 bv = __builtin_bit_cast(f16x8, *(const u32x4*)bsrc);
+      // A rows: centroid 16t + n; k-group 0 / 1 read ch, 2 reads cl, 3 the q row
+      const uint8_t* abase =
+          lds + (kg < 2 ? L.ch() + ((size_t)b * kVmNc + n) * 16
+                        : (kg == 2 ? L.cl() + ((size_t)b * kVmNc + n) * 16 : L.cq() + ((size_t)(b >> 2) * kVmNc + n) * 16));
+      typedef const __attribute__((address_space(3))) u32x4 LdsU32x4;
+      const LdsU32x4* ap = (const LdsU32x4*)abase;
+      const f32x4 acc0 = {init, init, init, init};
       uint32_t best = 0xffffffffu, second = 0xffffffffu;
+      // software pipelined: the product of tile t + 1 is issued before the
+      // keys of tile t are reduced
+      f32x4 acc_next = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, ap[0]), bv, acc0, 0, 0, 0);
 #pragma unroll
       for (int t = 0; t < 16; ++t) {
-        const float a0 = ct[32 * t];
-        const float a1 = ct[2 * (2 * kVmNc) + 32 * t];
-        const float csv = cs[16 * t];
-        const float a2 = kg == 0 ? csv : (kg == 1 ? 1.0f : 0.0f);
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b0, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b1, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a2, b2, acc, 0, 0, 0);
+        const f32x4 acc = acc_next;
+        if (t + 1 < 16)
+          acc_next = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, ap[16 * (t + 1)]), bv, acc0, 0, 0, 0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           // centroid 16t + 4kg + i of token n; low 6 bits = (t, i)
           const uint32_t key = (fbits(acc[i]) & 0xffffffc0u) | (uint32_t)(4 * t + i);
-          second = min(second, max(best, key));
+          second = med3_u32(best, second, key);
           best = min(best, key);
         }
       }
@@ -196,8 +322,8 @@ __global__ __launch_bounds__(kVmThreads) void encode_blockvq_mfma_kernel(
       const float vb = bitsf(gbest & 0xffffffc0u), vs = bitsf(gsecond & 0xffffffc0u);
       // clear winner: the runner-up more than delta behind (keys are
       // truncated by at most 2^-17 relative); distances positive and finite
-      const bool clear = (vs - vb * (1.0f + 0x1p-16f) > delta) && vb > 0.0f && vb < 3.0e38f &&
-                         delta < 3.0e38f;
+      const bool clear = (vs - vb * (1.0f + 0x1p-16f) > delta_s) && vb > 0.0f && vb < 3.0e38f &&
+                         delta_s < 3.0e38f;
       const int kw = best == gbest ? kg : 4;  // the lane holding the winner
       int kwin = kw;
       kwin = min(kwin, __shfl_xor(kwin, 16, 64));
@@ -219,12 +345,13 @@ __global__ __launch_bounds__(kVmThreads) void encode_blockvq_mfma_kernel(
 #pragma unroll
         for (int e = 0; e < kVmBd; ++e) xsq = xsq + x[e] * x[e];  // x.pow(2).sum(-1) order
         bool tie;
-        const int ci = exact_argmin(x, xsq, ct_all + b * kCtBlock, csq_all + b * kVmNc, lane, &tie);
+        const int ci = exact_argmin(x, xsq, C + (int64_t)b * kVmNc * kVmBd, lane, &tie);
         if (n == t0) idx = ci;
         if (lane == t0) ties += tie ? 1u : 0u;
       }
       if (valid && kg == 0) idx_out[row * nb + b] = (uint8_t)idx;
     }
+    kr = kr_next;
   }
   add_count(tie_count, ties);
 }
@@ -240,7 +367,7 @@ bool encode_blockvq_mfma_supported(int nb, int bd, int nc, const void* k, int kd
 }
 
 size_t encode_blockvq_mfma_lds(int nb) {
-  return (size_t)nb * (kCtBlock + kVmNc + 64 + 1) * sizeof(float);
+  return VmLds{nb}.bytes();
 }
 
 int launch_encode_blockvq_mfma(int kdtype, const void* k, RowMap map, int64_t rows, int nb,
@@ -253,7 +380,7 @@ int launch_encode_blockvq_mfma(int kdtype, const void* k, RowMap map, int64_t ro
   const int64_t want = (n_tiles + kVmWaves - 1) / kVmWaves;
   const unsigned grid = (unsigned)(want < cus ? want : cus);
   const size_t lds = encode_blockvq_mfma_lds(nb);
-  // the codebook takes more than the default 64 KB of dynamic LDS
+  // the split codebook takes more than the default 64 KB of dynamic LDS
   switch (kdtype) {
     case SMAQ_F32:
       hipFuncSetAttribute((const void*)encode_blockvq_mfma_kernel<float>,

@@ -357,6 +357,9 @@ struct Plan {
   int64_t hist_split, recent_split;
   int s_hist, s_recent;
   bool mfma, prefill;
+  // matrix-core decode with one workgroup per (sequence, KV head) and
+  // per-sequence lengths: dispatch the longest sequences first
+  bool longest_first;
   int64_t hist_lp, recent_lp;  // prefill plane lengths
 };
 
@@ -389,7 +392,22 @@ static Plan make_plan(const smaq_attn_params* p) {
   }
   pl.s_hist = hl > 0 ? (int)((hl + pl.hist_split - 1) / pl.hist_split) : 0;
   pl.s_recent = rl > 0 ? (int)((rl + pl.recent_split - 1) / pl.recent_split) : 0;
+  // With ragged lengths and a single split per sequence the workgroups differ
+  // in length by up to max / min; dispatched in batch order, the long ones
+  // that start late leave the GPU mostly idle at the end (measured: 256
+  // sequences U[1024, 16384] take 0.46 ms in batch order, 0.40 ms longest
+  // first).  More splits instead cost more than they balance: each
+  // workgroup's start is a chain of dependent memory round trips.
+  pl.longest_first = pl.mfma && p->hist_len != nullptr && pl.s_hist == 1 && p->batch > 1;
   return pl;
+}
+
+// Bytes of the partials (m, l, o) and the offset of the longest-first order.
+static int64_t partial_bytes(const smaq_attn_params* p, const Plan& pl) {
+  const int64_t S = pl.s_hist + pl.s_recent;
+  const int64_t rows = (int64_t)p->q_len * (p->n_q_heads / p->n_kv_heads);
+  const int64_t n = (int64_t)p->batch * p->n_kv_heads * rows * (S > 0 ? S : 1);
+  return n * (p->head_dim + 2) * (int64_t)sizeof(float);
 }
 
 }  // namespace smaq
@@ -399,10 +417,8 @@ using namespace smaq;
 extern "C" long long smaq_attn_workspace_bytes(const smaq_attn_params* p) {
   if (!p || p->n_kv_heads <= 0 || p->n_q_heads % p->n_kv_heads) return -1;
   const Plan pl = make_plan(p);
-  const int64_t S = pl.s_hist + pl.s_recent;
-  const int64_t rows = (int64_t)p->q_len * (p->n_q_heads / p->n_kv_heads);
-  const int64_t n = (int64_t)p->batch * p->n_kv_heads * rows * (S > 0 ? S : 1);
-  int64_t bytes = n * (p->head_dim + 2) * (int64_t)sizeof(float);
+  int64_t bytes = partial_bytes(p, pl);
+  if (pl.longest_first) bytes = align256(bytes) + (int64_t)p->batch * (int64_t)sizeof(int);
   if (pl.prefill) {
     // four f16 planes (key hi/lo, value hi/lo) per part
     const int64_t per_tok = (int64_t)p->batch * p->n_kv_heads * p->head_dim * 4 * 2;
@@ -520,7 +536,12 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
                p.block_size, p.n_kv_heads};
     int rc = SMAQ_EUNSUPPORTED;
     if (pl.mfma) {
-      rc = launch_mfma_decode(p, a, part, pl.hist_split, pl.s_hist, st);
+      int* order = nullptr;
+      if (pl.longest_first) {
+        order = (int*)((char*)p.workspace + align256(partial_bytes(&p, pl)));
+        if ((rc = launch_decode_order(p, order, st)) != SMAQ_OK) return rc;
+      }
+      rc = launch_mfma_decode(p, a, part, pl.hist_split, pl.s_hist, order, st);
       if (rc != SMAQ_OK) return rc;
     } else if (p.key_format == SMAQ_KEY_SCALAR) {
       switch (p.norm_dtype) {

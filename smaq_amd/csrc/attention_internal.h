@@ -64,7 +64,11 @@ int launch_prefill_mfma(const smaq_attn_params& p, const PrefillPart& pp, int n_
 // these parameters (history only, decode shape, supported formats).
 bool mfma_decode_supported(const smaq_attn_params& p);
 int64_t mfma_decode_split_len(const smaq_attn_params& p);
+// `order` (NULL: sequence b runs as grid row b) lists the sequences in the
+// order their workgroups are dispatched; launch_decode_order fills it with
+// the sequences by history length, longest first.
+int launch_decode_order(const smaq_attn_params& p, int* order, hipStream_t st);
 int launch_mfma_decode(const smaq_attn_params& p, const HistAddr& a, const Partials& part,
-                       int64_t split_len, int n_splits, hipStream_t st);
+                       int64_t split_len, int n_splits, const int* order, hipStream_t st);
 
 }  // namespace smaq

@@ -219,7 +219,7 @@ struct NormPair {
 
 template <int KBITS, typename TN, typename TV, bool SPLIT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWaves<TN, TV>, kDecodeWaves<TN, TV>))) void decode_mfma_kernel(
-    smaq_attn_params p, HistAddr addr, Partials part, int64_t split_len) {
+    smaq_attn_params p, HistAddr addr, Partials part, int64_t split_len, const int* __restrict__ order) {
   // key LUT, one 8-byte entry per code byte: {f16 hi pair, f16 lo pair}
   // (read with ds_read_b64, twice the rate of two dword reads)
   __shared__ __attribute__((aligned(16))) u32x2 lut[256];
@@ -242,7 +242,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
   // this lane's two softmax tokens: C-layout values 2*bank, 2*bank + 1
   const int tokA = bank < 2 ? 4 * kg + 2 * bank : 16 + 4 * kg + 2 * (bank - 2);
   const int tq = lane & 7, pq = lane >> 3;           // value loader: tokens 4tq.., bytes 4pq..
-  const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int s = blockIdx.x, h = blockIdx.y;
+  const int b = order ? __builtin_amdgcn_readfirstlane(order[blockIdx.z]) : (int)blockIdx.z;
   const int Q = p.n_q_heads / p.n_kv_heads;  // query rows (decode: one token)
   constexpr uint32_t kMask = (1u << KBITS) - 1u;
   constexpr float kLog2e = 1.4426950408889634f;
@@ -759,6 +760,46 @@ bool mfma_decode_supported(const smaq_attn_params& p) {
            (uintptr_t)p.val_scales | (uintptr_t)p.val_zeros) & 15) == 0;
 }
 
+// Sequences by history length, longest first: a counting sort on 1024
+// length buckets by one workgroup (bucket order is deterministic; the order
+// within a bucket is not, and does not change any result: each workgroup
+// computes its own (sequence, head) partials).
+constexpr int kOrderBuckets = 1024;
+
+__global__ __launch_bounds__(kOrderBuckets) void decode_order_kernel(const long long* __restrict__ len,
+                                                                     long long max_len, int batch,
+                                                                     int* __restrict__ order) {
+  __shared__ int count[kOrderBuckets];
+  const int tid = threadIdx.x;
+  count[tid] = 0;
+  __syncthreads();
+  auto bucket = [&](int b) {
+    long long L = len[b];
+    L = L < 0 ? 0 : (L > max_len ? max_len : L);
+    return kOrderBuckets - 1 - (int)(L * (kOrderBuckets - 1) / max_len);  // longest -> 0
+  };
+  for (int b = tid; b < batch; b += kOrderBuckets) atomicAdd(&count[bucket(b)], 1);
+  __syncthreads();
+  // exclusive prefix sum of the counts (Hillis-Steele over the workgroup)
+  int v = count[tid];
+  for (int off = 1; off < kOrderBuckets; off <<= 1) {
+    __syncthreads();
+    const int add = tid >= off ? count[tid - off] : 0;
+    __syncthreads();
+    count[tid] += add;
+  }
+  __syncthreads();
+  count[tid] -= v;  // inclusive -> exclusive
+  __syncthreads();
+  for (int b = tid; b < batch; b += kOrderBuckets) order[atomicAdd(&count[bucket(b)], 1)] = b;
+}
+
+int launch_decode_order(const smaq_attn_params& p, int* order, hipStream_t st) {
+  hipLaunchKernelGGL(decode_order_kernel, dim3(1), dim3(kOrderBuckets), 0, st, p.hist_len,
+                     (long long)p.max_hist_len, p.batch, order);
+  return launch_status("smaq_attn_hybrid(decode order)");
+}
+
 int64_t mfma_decode_split_len(const smaq_attn_params& p) {
   const int64_t units = (int64_t)p.batch * p.n_kv_heads;
   const int64_t want = units >= 2048 ? 1 : (2048 + units - 1) / units;
@@ -770,37 +811,37 @@ int64_t mfma_decode_split_len(const smaq_attn_params& p) {
 
 template <int KB, typename TN, bool SPLIT>
 static void launch_v(const smaq_attn_params& p, const HistAddr& a, const Partials& part,
-                     int64_t split_len, int n_splits, hipStream_t st) {
+                     int64_t split_len, int n_splits, const int* order, hipStream_t st) {
   dim3 grid(n_splits, p.n_kv_heads, p.batch);
   switch (p.val_dtype) {
-    case SMAQ_F32: hipLaunchKernelGGL((decode_mfma_kernel<KB, TN, float, SPLIT>), grid, dim3(256), 0, st, p, a, part, split_len); break;
-    case SMAQ_F16: hipLaunchKernelGGL((decode_mfma_kernel<KB, TN, _Float16, SPLIT>), grid, dim3(256), 0, st, p, a, part, split_len); break;
-    default: hipLaunchKernelGGL((decode_mfma_kernel<KB, TN, bf16, SPLIT>), grid, dim3(256), 0, st, p, a, part, split_len); break;
+    case SMAQ_F32: hipLaunchKernelGGL((decode_mfma_kernel<KB, TN, float, SPLIT>), grid, dim3(256), 0, st, p, a, part, split_len, order); break;
+    case SMAQ_F16: hipLaunchKernelGGL((decode_mfma_kernel<KB, TN, _Float16, SPLIT>), grid, dim3(256), 0, st, p, a, part, split_len, order); break;
+    default: hipLaunchKernelGGL((decode_mfma_kernel<KB, TN, bf16, SPLIT>), grid, dim3(256), 0, st, p, a, part, split_len, order); break;
   }
 }
 
 template <int KB, typename TN>
 static void launch_s(const smaq_attn_params& p, const HistAddr& a, const Partials& part,
-                     int64_t split_len, int n_splits, hipStream_t st) {
+                     int64_t split_len, int n_splits, const int* order, hipStream_t st) {
   // 16-token pages put a tile's two 16-token groups in different blocks
-  if (p.block_table && p.block_size == 16) launch_v<KB, TN, true>(p, a, part, split_len, n_splits, st);
-  else launch_v<KB, TN, false>(p, a, part, split_len, n_splits, st);
+  if (p.block_table && p.block_size == 16) launch_v<KB, TN, true>(p, a, part, split_len, n_splits, order, st);
+  else launch_v<KB, TN, false>(p, a, part, split_len, n_splits, order, st);
 }
 
 template <int KB>
 static void launch_n(const smaq_attn_params& p, const HistAddr& a, const Partials& part,
-                     int64_t split_len, int n_splits, hipStream_t st) {
+                     int64_t split_len, int n_splits, const int* order, hipStream_t st) {
   switch (p.norm_dtype) {
-    case SMAQ_F32: launch_s<KB, float>(p, a, part, split_len, n_splits, st); break;
-    case SMAQ_F16: launch_s<KB, _Float16>(p, a, part, split_len, n_splits, st); break;
-    default: launch_s<KB, bf16>(p, a, part, split_len, n_splits, st); break;
+    case SMAQ_F32: launch_s<KB, float>(p, a, part, split_len, n_splits, order, st); break;
+    case SMAQ_F16: launch_s<KB, _Float16>(p, a, part, split_len, n_splits, order, st); break;
+    default: launch_s<KB, bf16>(p, a, part, split_len, n_splits, order, st); break;
   }
 }
 
 int launch_mfma_decode(const smaq_attn_params& p, const HistAddr& a, const Partials& part,
-                       int64_t split_len, int n_splits, hipStream_t st) {
-  if (p.key_bits == 3) launch_n<3>(p, a, part, split_len, n_splits, st);
-  else launch_n<4>(p, a, part, split_len, n_splits, st);
+                       int64_t split_len, int n_splits, const int* order, hipStream_t st) {
+  if (p.key_bits == 3) launch_n<3>(p, a, part, split_len, n_splits, order, st);
+  else launch_n<4>(p, a, part, split_len, n_splits, order, st);
   return launch_status("smaq_attn_hybrid(mfma decode)");
 }
 

@@ -74,6 +74,56 @@ def test_mfma_decode_paged(dev):
         assert_attn_close(out[b:b + 1], _oracle(codec, keys[b], vals[b], q[b:b + 1], 32, 8), f"paged mfma {b}")
 
 
+def test_mfma_decode_paged_longest_first(dev):
+    """256 ragged sequences x 8 KV heads = 2048 (sequence, head) units: one
+    workgroup each, dispatched longest sequence first through an order the
+    library writes into the plan's workspace (its size shows the path is
+    taken).  Every sequence matches the generic kernels (batch order) and a
+    sample, including the longest and the shortest, matches the oracle."""
+    strat, codec = _codec_pair(dev, 3, 300)
+    gen = torch.Generator().manual_seed(301)
+    B, bs, hkv = 256, 16, 8
+    lens = [int(x) for x in torch.randint(1, 160, (B,), generator=gen)]
+    lens[7], lens[200] = 900, 1
+    nblk = [(n + bs - 1) // bs for n in lens]
+    nphys = sum(nblk) + 5
+    perm = torch.randperm(nphys, generator=gen)
+    table = torch.zeros(B, max(nblk), dtype=torch.int32)
+    o = 0
+    for b, nb in enumerate(nblk):
+        table[b, :nb] = perm[o:o + nb].to(torch.int32)
+        o += nb
+    allk = sample_keys(sum(lens) * hkv, seed=302).reshape(sum(lens), hkv, 128).bfloat16()
+    allv = torch.randn(sum(lens), hkv, 128, generator=gen).bfloat16()
+    cut = [0]
+    for n in lens:
+        cut.append(cut[-1] + n)
+    keys = [allk[cut[b]:cut[b + 1]] for b in range(B)]
+    vals = [allv[cut[b]:cut[b + 1]] for b in range(B)]
+    pk = PagedQuantizedKV.encode(strat, [k.to(dev) for k in keys], [v.to(dev) for v in vals], table.to(dev),
+                                 num_blocks=nphys, block_size=bs)
+    q = torch.randn(B, 32, 128, generator=gen).bfloat16()
+    plan = pk.plan(q.to(dev), impl=2)
+    partials = B * hkv * 4 * (128 + 2) * 4          # one split: (m, l, o) per query row
+    assert plan.workspace.numel() == partials + B * 4, "longest-first order not planned"
+    out = plan.run(q.to(dev)).squeeze(1).clone()
+    again = plan.run(q.to(dev)).squeeze(1)
+    assert torch.equal(out, again)
+    out_g = pk.attention(q.to(dev), impl=1)
+    assert_attn_close(out, out_g.cpu(), "longest first vs generic (all sequences)")
+    # the oracle's store API ignores histories under MIN_HISTORY_FOR_SMAQ
+    # tokens (smaq/score.py:38); the batched path attends every history, so
+    # the sample is drawn from sequences of 16+ tokens ...
+    for b in [7] + [b for b in range(B) if lens[b] >= 16][:4]:
+        assert_attn_close(out[b:b + 1], _oracle(codec, keys[b], vals[b], q[b:b + 1], 32, hkv),
+                          f"longest first seq {b} len {lens[b]}")
+    # ... and the 1-token history attends its one token: the output is that
+    # token's dequantised value for each query head of the group
+    vq = R.quantize_values(vals[200].permute(1, 0, 2).unsqueeze(0), bits=2, group_size=32)
+    v_hat = R.dequantize_values(vq, 32)[0, :, 0, :].repeat_interleave(32 // hkv, dim=0)
+    assert_attn_close(out[200:201], v_hat.unsqueeze(0).bfloat16(), "longest first seq 200 len 1")
+
+
 def test_mfma_decode_peaked_scores(dev):
     """Large query norms (sharp softmax): the hi/lo splits keep scores exact
     enough that the winning tokens' weights match."""

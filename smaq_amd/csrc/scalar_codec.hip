@@ -317,11 +317,7 @@ extern "C" int smaq_rotate_rows(const void* x, int xdtype, long long rows, int D
   const int64_t blocks = ((int64_t)rows + kRotRows - 1) / kRotRows;
   SMAQ_REQUIRE(blocks < (1ll << 31), "smaq_rotate_rows: too many rows");
   hipStream_t st = (hipStream_t)stream;
-  // head_dim 128: two rows per workgroup while that is needed to fill the
-  // GPU; from 4096 rows the 8-row kernel below, whose Mt loads each feed 8
-  // chains (2 rows per workgroup re-read the 64 KB matrix for every pair of
-  // rows: 8192 rows took 21.7 us).  Both run the same fmaf chain per output.
-  if (D == 128 && rows < 4096) {
+  if (D == 128) {
     SMAQ_REQUIRE((rows + 1) / 2 < (1ll << 31), "smaq_rotate_rows: too many rows");
     SMAQ_DISPATCH_DTYPE(xdtype, T,
         hipLaunchKernelGGL(rotate_rows128_kernel<T>, dim3((unsigned)((rows + 1) / 2)), dim3(256), 0, st,

@@ -152,6 +152,32 @@ def test_scalar_dequant_scores_rotate(dev):
     torch.testing.assert_close(raw.cpu(), R.smaq_scores(query[0], ref, c, Ei, 128), atol=2e-3, rtol=1e-4)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("scaled", [False, True])
+def test_rotate_rows_128_chunking_and_accuracy(dev, dtype, scaled):
+    """smaq_rotate_rows at head_dim 128 (the decode query rotation): one
+    sequential fmaf chain per output, so 5000 rows in one call equal the same
+    rows in two calls of 2500 bit for bit, and match the float64 product
+    within the rounding bound of a 128-term fp32 chain."""
+    g = torch.Generator().manual_seed(130)
+    M = torch.linalg.qr(torch.randn(128, 128, generator=g, dtype=torch.float64))[0].float()
+    cs = (torch.rand(128, generator=g) + 0.5) if scaled else None
+    x = torch.randn(5000, 128, generator=g).to(dtype)
+    Mt, csd = M.T.contiguous().to(dev), None if cs is None else cs.to(dev)
+    xd = x.to(dev)
+    whole = torch.empty(5000, 128, device=dev)
+    _native.rotate_rows_into(xd, Mt, csd, whole)
+    parts = torch.empty(5000, 128, device=dev)
+    _native.rotate_rows_into(xd[:2500], Mt, csd, parts[:2500])
+    _native.rotate_rows_into(xd[2500:], Mt, csd, parts[2500:])
+    assert torch.equal(whole, parts)
+    ref = x.double() @ M.T.double()
+    if cs is not None:
+        ref = ref * cs.double()
+    bound = 128 * 2.0 ** -24 * (x.double().abs() @ M.T.double().abs()) * (1.0 if cs is None else cs.double() * 2)
+    assert bool(((whole.cpu().double() - ref).abs() <= bound + 1e-30).all())
+
+
 def _vq_setup(nb=16, bd=8, nc=256, seed=0, n_fit=4096):
     keys = sample_keys(n_fit, seed=seed + 80)
     queries = sample_keys(n_fit, seed=seed + 81)

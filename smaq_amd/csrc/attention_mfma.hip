@@ -463,6 +463,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
     typedef const __attribute__((address_space(3))) u32x4 LdsU32x4;
     const LdsU32x4* bqp = (const LdsU32x4*)&bqs[0][lane];
     asm volatile("" : "+v"(bqp));  // read each tile (keeps the operands out of registers)
+    // The matrix sections run at raised wave priority: the four waves of a
+    // SIMD drift apart (no workgroup barrier in the loop), and letting the
+    // wave in its MFMA chain issue first while the others fill in VALU work
+    // measured 2% faster (0.1928 -> 0.1884 ms at c3).
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int st = 0; st < 8; ++st) {
       const u32x4 bqv = bqp[64 * st];
@@ -475,6 +480,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
       ca = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(av), as_f16x8(bqv), ca, 0, 0, 0);
       cb = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(bv), as_f16x8(bqv), cb, 0, 0, 0);
     }
+    __builtin_amdgcn_s_setprio(0);
     after_keys();
     // -- scores.  C layout: lane (kg, n) holds column n for tokens 4kg + v (ca)
     // and 16 + 4kg + v (cb).  Add the lo column n + 8 (row_shl:8), then move
@@ -558,6 +564,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
     const u32x4 alo = *(const u32x4*)(ar + 64);
     const u32x4 w0 = *(const u32x4*)(vr);
     const u32x4 w1 = *(const u32x4*)(vr + kVRow * 16);
+    __builtin_amdgcn_s_setprio(1);
     acc_s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ahi), as_bf16x8(kOnesBf16), acc_s, 0, 0, 0);
     acc_s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(alo), as_bf16x8(kOnesBf16), acc_s, 0, 0, 0);
 #pragma unroll
@@ -571,6 +578,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
       acc_o[tau] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ahi), as_bf16x8(bv), acc_o[tau], 0, 0, 0);
       acc_o[tau] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(alo), as_bf16x8(bv), acc_o[tau], 0, 0, 0);
     }
+    __builtin_amdgcn_s_setprio(0);
     wave_sync();  // this tile's LDS reads complete before the next tile's writes
   };
 

@@ -5,10 +5,18 @@
 // torch-CPU does for bf16/fp16 tensors (compute in fp32, round once, RNE):
 //   range = rnd(max - min); scale = rnd(range / levels)  (true division)
 //   scale = max(scale, rnd(1e-10))  -- clamp bound converted to the dtype
+//   min / max propagate NaN (torch's reductions)
 //   code  = clamp(rint(rnd(rnd(v - min) / scale)), 0, levels), NaN -> 0
+#include <type_traits>
+
 #include "smaq_common.h"
 
 namespace smaq {
+
+// Group minimum / maximum as torch's min / max reductions: a NaN anywhere in
+// the group is the result (v_minimum3_f32 / v_maximum3_f32 on gfx950).
+__device__ __forceinline__ float nan_min(float a, float b) { return __builtin_elementwise_minimum(a, b); }
+__device__ __forceinline__ float nan_max(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 
 // Codes stored per byte: 2-bit -> 4, 4-bit -> 2, other widths unpacked.
 __host__ __device__ __forceinline__ int value_codes_per_byte(int bits) {
@@ -40,8 +48,8 @@ __global__ __launch_bounds__(256) void pack_values_kernel(
     float hi = lo;
     for (int e = 1; e < group; ++e) {
       const float x = Num<T>::to_f(gp[e]);
-      lo = fminf(lo, x);
-      hi = fmaxf(hi, x);
+      lo = nan_min(lo, x);
+      hi = nan_max(hi, x);
     }
     float sc = Num<T>::round(Num<T>::round(hi - lo) / levels);
     if (sc < min_scale) sc = min_scale;  // clamp(min=1e-10), NaN passes
@@ -97,20 +105,39 @@ __global__ __launch_bounds__(256) void pack_values_g32_kernel(
   float lo = x[0], hi = x[0];
 #pragma unroll
   for (int e = 1; e < kG; ++e) {
-    lo = fminf(lo, x[e]);
-    hi = fmaxf(hi, x[e]);
+    lo = nan_min(lo, x[e]);
+    hi = nan_max(hi, x[e]);
   }
   float sc = Num<T>::round(Num<T>::round(hi - lo) / levels);
   if (sc < min_scale) sc = min_scale;  // clamp(min=1e-10), NaN passes
   scales[row * n_groups + g] = Num<T>::from_f(sc);
   zeros[row * n_groups + g] = Num<T>::from_f(lo);
   uint32_t out[4] = {0u, 0u, 0u, 0u};
+  if constexpr (std::is_same<T, bf16>::value) {
+    // bf16: a / sc as a * RN(1 / sc), with the roundings to bf16 done by the
+    // hardware conversion (RNE).  Same codes as the division: a and sc carry
+    // 8-bit significands, so a / sc is never a bf16 rounding midpoint (that
+    // needs a 9-bit numerator) and lies at least 2^-17 (relative) from every
+    // midpoint, while a * RN(1 / sc) is within 2^-23 of it; both round to
+    // the same bf16 value, hence the same code.  NaN and infinities give the
+    // same NaN / 0 quotients as the division (inf * 0, x * 0).
+    const float rs = 1.0f / sc;
 #pragma unroll
-  for (int e = 0; e < kG; ++e) {
-    float q = round_half_even(Num<T>::round(Num<T>::round(x[e] - lo) / sc));
-    q = fminf(fmaxf(q, 0.0f), levels);
-    const uint32_t code = (q == q) ? (uint32_t)q : 0u;  // NaN -> 0
-    out[e / (4 * vpb)] |= code << (BITS * (e % (4 * vpb)));
+    for (int e = 0; e < kG; ++e) {
+      const float a = (float)(__bf16)(x[e] - lo);
+      float q = round_half_even((float)(__bf16)(a * rs));
+      q = fminf(fmaxf(q, 0.0f), levels);
+      const uint32_t code = (q == q) ? (uint32_t)q : 0u;  // NaN -> 0
+      out[e / (4 * vpb)] |= code << (BITS * (e % (4 * vpb)));
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < kG; ++e) {
+      float q = round_half_even(Num<T>::round(Num<T>::round(x[e] - lo) / sc));
+      q = fminf(fmaxf(q, 0.0f), levels);
+      const uint32_t code = (q == q) ? (uint32_t)q : 0u;  // NaN -> 0
+      out[e / (4 * vpb)] |= code << (BITS * (e % (4 * vpb)));
+    }
   }
   uint8_t* dst = data + row * (n_groups * kG / vpb) + g * (kG / vpb);
   if constexpr (BITS == 2) *(uint2*)dst = uint2{out[0], out[1]};

@@ -42,6 +42,40 @@ def test_pack_values_bit_exact(dev, dtype, bits, T):
     assert torch.equal(back, R.dequantize_values(ref, 32))
 
 
+@pytest.mark.parametrize("bits", [2, 4])
+def test_pack_values_bf16_wide_range(dev, bits):
+    """The bf16 group-32 packer divides by multiplying with RN(1 / scale);
+    the codes must still equal the true division's on every row: 65536 rows
+    at magnitudes 1e-35..1e35, constant rows, two-level rows, exact multiples
+    of the step, subnormal and non-finite values."""
+    g = torch.Generator().manual_seed(140 + bits)
+    n = 65536
+    mag = torch.pow(10.0, torch.empty(n, 1).uniform_(-35, 35, generator=g))
+    v = torch.randn(n, 128, generator=g) * mag
+    v[:512] = 3.25                                                   # constant groups
+    v[512:1024] = torch.where(torch.rand(512, 128, generator=g) < 0.5, -1.0, 2.0)   # two levels
+    step = torch.pow(2.0, torch.randint(-10, 10, (1024, 1), generator=g).float())
+    lev = (1 << bits) - 1
+    v[1024:2048] = torch.randint(0, 4 * lev + 1, (1024, 128), generator=g).float() * step / 4   # multiples
+    v[2048:2560] = torch.randn(512, 128, generator=g) * 1e-39        # subnormal in bf16
+    v[2560, 5] = float("nan")
+    v[2561, 40] = float("inf")
+    v[2562, 70] = -float("inf")
+    vb = v.bfloat16()
+    ref = R.quantize_values(vb, bits=bits, group_size=32)
+    got = S.quantize_values(vb.to(dev), bits=bits, group_size=32)
+    bad = (got.data.cpu() != ref.data).any(1)
+    assert not bad.any(), f"{int(bad.sum())} rows differ, first {int(bad.nonzero()[0])}"
+    # scales / zeros bit for bit, a NaN matching any NaN: the NaN group's
+    # payload comes from the host CPU's vector min (0x7fc0 on one machine,
+    # 0xffff on another), the kernel writes the canonical 0x7fc0
+    for name in ("scales", "zeros"):
+        a, b = getattr(got, name).cpu(), getattr(ref, name)
+        an, bn = a.isnan(), b.isnan()
+        assert torch.equal(an, bn) and int(an.sum()) == 1, name
+        assert torch.equal(a[~an].view(torch.int16), b[~bn].view(torch.int16)), name
+
+
 @pytest.mark.parametrize("group", [16, 64, 128])
 def test_pack_values_groups(dev, group):
     v = torch.randn(3, 50, 128, generator=torch.Generator().manual_seed(group)).bfloat16()

@@ -212,15 +212,17 @@ __global__ __launch_bounds__(kVmThreads) void encode_blockvq_mfma_kernel(
     if (b < nb) {
       const float sg = sig_all[b];
       const float* cc = C + ((int64_t)b * kVmNc + c) * kVmBd;
+      // dims in K-slot order [0, 4, 1, 5, 2, 6, 3, 7]: slots 2i, 2i + 1 hold
+      // dims i, i + 4, the two shaped-key dims one k-group lane computes
       uint32_t hw[4], lw[4];
       float q = 0.0f;
 #pragma unroll
-      for (int e = 0; e < kVmBd; e += 2) {
-        const float v0 = cc[e] * sg, v1 = cc[e + 1] * sg;
+      for (int i = 0; i < 4; ++i) {
+        const float v0 = cc[i] * sg, v1 = cc[i + 4] * sg;
         const _Float16 h0 = (_Float16)v0, h1 = (_Float16)v1;
         const _Float16 l0 = (_Float16)(v0 - (float)h0), l1 = (_Float16)(v1 - (float)h1);
-        hw[e >> 1] = h16(h0) | (h16(h1) << 16);
-        lw[e >> 1] = h16(l0) | (h16(l1) << 16);
+        hw[i] = h16(h0) | (h16(h1) << 16);
+        lw[i] = h16(l0) | (h16(l1) << 16);
         q = fmaf(v0, v0, q);
         q = fmaf(v1, v1, q);
       }
@@ -235,8 +237,19 @@ __global__ __launch_bounds__(kVmThreads) void encode_blockvq_mfma_kernel(
   __syncthreads();
 
   const int n = lane & 15, kg = lane >> 4;  // MFMA coordinates: token / centroid row n, k-group kg
-  uint8_t* const ys_w = lds + L.ys() + (size_t)w * 16 * 32;
-  _Float16* const ys_tok = (_Float16*)(ys_w + n * 32);  // this lane's token: y hi [8] | y lo [8]
+  // LDS addressing in 32 bits
+  typedef __attribute__((address_space(3))) uint8_t LdsByte;
+  typedef const __attribute__((address_space(3))) u32x4 LdsU32x4;
+  typedef const __attribute__((address_space(3))) f32x4 LdsF32x4;
+  LdsByte* const lds3 = (LdsByte*)lds;
+  // this lane's token: y hi [8] | y lo [8] in K-slot order; the lane owns
+  // slots 2kg, 2kg + 1 of each half
+  const uint32_t ys_tok = (uint32_t)(L.ys() + (size_t)w * 16 * 32 + n * 32);
+  // B operand source (k-group 0 / 2: y hi, 1: y lo, 3: the |C|^2 pair row)
+  const uint32_t b_src = kg == 3 ? (uint32_t)L.bq() : ys_tok + (kg == 1 ? 16u : 0u);
+  // A rows: centroid 16t + n; k-group 0 / 1 read ch, 2 reads cl, 3 the q row
+  const uint32_t a_src = kg < 2 ? (uint32_t)(L.ch() + n * 16) : (kg == 2 ? (uint32_t)(L.cl() + n * 16) : (uint32_t)(L.cq() + n * 16));
+  const uint32_t a_blk = kg < 3 ? (uint32_t)(kVmNc * 16) : 0u;  // A bytes per block (q rows: per 4 blocks)
   unsigned ties = 0;
   const int64_t n_tiles = (rows + 15) / 16;
   const int64_t stride = (int64_t)gridDim.x * kVmWaves;
@@ -259,22 +272,25 @@ __global__ __launch_bounds__(kVmThreads) void encode_blockvq_mfma_kernel(
       next.unpack(kv);
       // the next key block of this lane's token (or the next tile's first)
       next.load(b + 1 < nb ? kr + (b + 1) * kVmBd : kr_next);
-      const float* es = es_all + b * 64;
+      // rows kg and kg + 4 of E_b, 16-byte reads
+      const LdsF32x4* er = (const LdsF32x4*)(lds3 + L.es() + (size_t)b * 256 + kg * 32);
+      const f32x4 ea0 = er[0], ea1 = er[1], eb0 = er[8], eb1 = er[9];  // row kg + 4: 128 bytes on
+      const float ea[kVmBd] = {ea0[0], ea0[1], ea0[2], ea0[3], ea1[0], ea1[1], ea1[2], ea1[3]};
+      const float eb[kVmBd] = {eb0[0], eb0[1], eb0[2], eb0[3], eb1[0], eb1[1], eb1[2], eb1[3]};
       // x_kg and x_{kg+4}: the reference's chain, bit for bit
       float xa = 0.0f, xb = 0.0f;
 #pragma unroll
       for (int d = 0; d < kVmBd; ++d) {
-        xa = fmaf(kv[d], es[kg * 8 + d], xa);
-        xb = fmaf(kv[d], es[(kg + 4) * 8 + d], xb);
+        xa = fmaf(kv[d], ea[d], xa);
+        xb = fmaf(kv[d], eb[d], xb);
       }
       const float sg = sig_all[b];
       const float ya = xa * (-2.0f * sg), yb = xb * (-2.0f * sg);  // exact (powers of two)
       const bool ok = fabsf(ya) < kYMax && fabsf(yb) < kYMax;     // false for NaN
       const _Float16 yah = (_Float16)ya, ybh = (_Float16)yb;
-      ys_tok[kg] = yah;
-      ys_tok[kg + 4] = ybh;
-      ys_tok[8 + kg] = (_Float16)(ya - (float)yah);
-      ys_tok[8 + kg + 4] = (_Float16)(yb - (float)ybh);
+      const _Float16 yal = (_Float16)(ya - (float)yah), ybl = (_Float16)(yb - (float)ybh);
+      *(__attribute__((address_space(3))) uint32_t*)(lds3 + ys_tok + 4 * kg) = h16(yah) | (h16(ybh) << 16);
+      *(__attribute__((address_space(3))) uint32_t*)(lds3 + ys_tok + 16 + 4 * kg) = h16(yal) | (h16(ybl) << 16);
       float sq = ok ? xa * xa + xb * xb : __builtin_nanf("");
       sq += __shfl_xor(sq, 16, 64);
       sq += __shfl_xor(sq, 32, 64);
@@ -284,14 +300,10 @@ __global__ __launch_bounds__(kVmThreads) void encode_blockvq_mfma_kernel(
       const float delta_s = delta * s2;
       wave_sync();
       // B: k-group 0 / 2 take y hi, 1 takes y lo, 3 the 2^14 pair of block b
-      const uint8_t* bsrc = kg == 3 ? lds + L.bq() + (b & 3) * 16 : (const uint8_t*)ys_tok + (kg == 1 ? 16 : 0);
-      const f16x8 bv = __builtin_bit_cast(f16x8, *(const u32x4*)bsrc);
-      // A rows: centroid 16t + n; k-group 0 / 1 read ch, 2 reads cl, 3 the q row
-      const uint8_t* abase =
-          lds + (kg < 2 ? L.ch() + ((size_t)b * kVmNc + n) * 16
-                        : (kg == 2 ? L.cl() + ((size_t)b * kVmNc + n) * 16 : L.cq() + ((size_t)(b >> 2) * kVmNc + n) * 16));
-      typedef const __attribute__((address_space(3))) u32x4 LdsU32x4;
-      const LdsU32x4* ap = (const LdsU32x4*)abase;
+      const f16x8 bv = __builtin_bit_cast(
+          f16x8, *(LdsU32x4*)(lds3 + b_src + (kg == 3 ? (uint32_t)(b & 3) * 16u : 0u)));
+      const LdsU32x4* ap =
+          (LdsU32x4*)(lds3 + a_src + (kg < 3 ? (uint32_t)b * a_blk : (uint32_t)(b >> 2) * (uint32_t)(kVmNc * 16)));
       const f32x4 acc0 = {init, init, init, init};
       uint32_t best = 0xffffffffu, second = 0xffffffffu;
       // software pipelined: the product of tile t + 1 is issued before the

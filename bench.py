@@ -186,6 +186,8 @@ def bench_paged(args, dev):
     ms_step = start.elapsed_time(end) / args.steps
     kern_ms = history_kernel_ms(plan, q, args.steps)
     achieved = algo / (kern_ms * 1e-3) / 1e9
+    cpu = None if args.no_cpu_baseline else cpu_baseline_paged(strat, table, lens, bs, codes, norms, vd, vsc, vz,
+                                                                  q, Hq, Hkv, D)
     return {
         "metric": METRIC,
         "value": B / (ms_step * 1e-3),
@@ -208,7 +210,7 @@ def bench_paged(args, dev):
                      "kernel": "decode_mfma_kernel",
                      "kernel_ms": kern_ms, "algorithmic_bytes": algo,
                      "bytes_per_token_head": pk.nbytes_per_token_head()},
-        "cpu_baseline": None,
+        "cpu_baseline": cpu,
         "extra": {"encode_boundary_ties": strat.quantizer.tie_counter.value()},
     }
 
@@ -269,6 +271,7 @@ def bench_prefill(args, dev):
     hist_pairs = sum(min(int(p) + 1, N) for p in pos.tolist()) * Hq
     hist_flops = hist_pairs * D * 2 * 2
     byts = N * Hkv * (64 + 32 + 8 + 8) + R * Hkv * D * 2 * 2 + T * Hq * D * 2 * 2
+    cpu = None if args.no_cpu_baseline else cpu_baseline_prefill(strat, st, kr, vr, q, pos, Hq, Hkv, D)
     return {
         "metric": METRIC,
         "value": T / (ms * 1e-3),
@@ -290,7 +293,7 @@ def bench_prefill(args, dev):
                      "kernel": "prefill_mfma_kernel (history phase, with decode_hist_planes_kernel)",
                      "kernel_ms": kern_ms, "algorithmic_flops": hist_flops, "step_flops": flops,
                      "step_tflops": flops / (ms * 1e-3) / 1e12, "algorithmic_bytes": byts},
-        "cpu_baseline": None,
+        "cpu_baseline": cpu,
     }
 
 
@@ -397,6 +400,77 @@ def cpu_baseline_encode(strat, keys, vals, n: int = 2048):
     t = statistics.median(times)
     return {"value": n * (2 * 256 + 64) / t / 1e9, "unit": "GB/s", "cores": _cores(), "kind": "port",
             "sample": f"{n} token-heads, median of 3 after 1 warm-up ({t * 1e3:.1f} ms)"}
+
+
+class _FlatStore:
+    """The oracle Store interface (what its hybrid_attention reads) over a
+    flat cache taken from the GPU pool, so that a CPU baseline times the
+    oracle's attention without re-encoding the history on the host."""
+
+    def __init__(self, flat, codec, head_dim, num_kv_heads, value_group_size=32):
+        self.flat, self.codec = flat, codec
+        self.head_dim, self.num_kv_heads, self.value_group_size = head_dim, num_kv_heads, value_group_size
+
+    def get_flat_cache(self):
+        return self.flat
+
+
+def _median_time(fn, reps: int = 3) -> float:
+    fn()  # warm-up
+    times = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+    return statistics.median(times)
+
+
+def cpu_baseline_paged(strat, table, lens, bs, codes, norms, vd, vsc, vz, q, Hq, Hkv, D):
+    """CPU oracle decoding the median-length sequence of the paged batch (all
+    KV heads), its codes gathered from the GPU pool; scaled to the batch by
+    total tokens / sample tokens (decode time is linear in the context)."""
+    from oracle import smaq_ref as R
+    b = int(torch.argsort(lens)[len(lens) // 2])
+    L = int(lens[b])
+    nb = (L + bs - 1) // bs
+    blocks = table[b, :nb].long().to(codes.device)
+
+    def gather(x):  # pool [blocks, Hkv, bs, ...] -> [Hkv, L, ...] on the host
+        y = x[blocks].transpose(0, 1).reshape(Hkv, nb * bs, *x.shape[3:])[:, :L]
+        return y.cpu().contiguous()
+
+    qz = strat.quantizer
+    codec = R.ScalarCodec(D, 3, E=qz.E.cpu(), E_inv=qz.E_inv.cpu())
+    flat = R.FlatCache(R.ScalarQ(gather(codes), gather(norms), 3),
+                       R.ValueQ(gather(vd), gather(vsc), gather(vz), 2), L)
+    st = _FlatStore(flat, codec, D, Hkv)
+    qc = q[b:b + 1].cpu()
+    t = _median_time(lambda: R.hybrid_attention(qc, st, None, None, Hq))
+    t_batch = t * float(lens.sum()) / L
+    return {"value": len(lens) / t_batch, "unit": "tokens/s", "cores": _cores(), "kind": "port",
+            "sample": f"sequence {b} ({L} tokens, the median length; all {Hkv} KV heads; codes from the GPU "
+                      f"pool), median of 3 after 1 warm-up, {t * 1e3:.1f} ms; scaled to the batch by "
+                      f"{int(lens.sum())} / {L} tokens"}
+
+
+def cpu_baseline_prefill(strat, st, kr, vr, q, pos, Hq, Hkv, D, n_q: int = 64):
+    """CPU oracle for the last n_q query tokens of the chunk (full causal
+    context: the block-VQ history from the GPU store plus the exact recent
+    window)."""
+    from oracle import smaq_ref as R
+    qz = strat.quantizer
+    codec = R.BlockVQCodec(qz.E_blocks.cpu(), qz.centroids.cpu(), qz.decoded_centroids.cpu())
+    gf = st.get_flat_cache()
+    flat = R.FlatCache(R.BlockQ(gf.key_q.indices.cpu(), gf.key_q.n_blocks, gf.key_q.block_dim),
+                       R.ValueQ(gf.value_q.data.cpu(), gf.value_q.scales.cpu(), gf.value_q.zeros.cpu(),
+                                gf.value_q.bits), gf.num_tokens)
+    ost = _FlatStore(flat, codec, D, Hkv)
+    qs, ps, krc, vrc = q[-n_q:].cpu(), pos[-n_q:].cpu(), kr.cpu(), vr.cpu()
+    t = _median_time(lambda: R.hybrid_attention(qs, ost, krc, vrc, Hq, query_positions=ps))
+    return {"value": n_q / t, "unit": "tokens/s", "cores": _cores(), "kind": "port",
+            "sample": f"the last {n_q} of {q.shape[0]} query tokens over the full context "
+                      f"({gf.num_tokens} history + {kr.shape[0]} recent), median of 3 after 1 warm-up, "
+                      f"{t * 1e3:.1f} ms"}
 
 
 def cpu_baseline_decode(strat, keys, vals, q, Hq, Hkv, D, bits):

@@ -281,6 +281,28 @@ def test_blockvq_encode_matrix_core_large(dev, dtype):
     assert torch.equal(got_v[0].transpose(0, 1).reshape(40000, 16), got)
 
 
+@pytest.mark.parametrize("scale", [1e-6, 1.0, 1e6])
+def test_blockvq_encode_matrix_core_ranges(dev, scale):
+    """The matrix-core encoder on 8 blocks (head_dim 64), a codebook far from
+    unit scale (the per-block power-of-two rescaling) and keys whose shaped
+    components exceed the f16 operand range (|x| > 2^13 / sigma: those pairs
+    take the exact recount): indices as the oracle's up to counted ties."""
+    D, nb = 64, 8
+    keys0 = sample_keys(4096, seed=150)[:, :D] * scale
+    Eb, Eib, C, Dc = R.blockvq_fit(keys0, sample_keys(4096, seed=151)[:, :D] * scale, block_dim=8,
+                                   n_centroids=256, iters=3, seed=42)
+    vq = S.SMAQBlockVQ(D, block_dim=8, device=dev)
+    vq.E_blocks, vq.E_inv_blocks = Eb.to(dev), Eib.to(dev)
+    vq.centroids, vq.decoded_centroids = C.to(dev), Dc.to(dev)
+    keys = sample_keys(6000, seed=152)[:, :D] * scale
+    keys[::7] *= 3.0e4          # shaped components far beyond the codebook's range
+    keys[3, :8] = 0.0           # an all-zero block
+    ref = R.blockvq_encode(keys, Eb, C).indices
+    vq.tie_counter = _native.TieCounter(dev)
+    got = vq.quantize(keys.to(dev)).indices.cpu().long()
+    _check_vq_against_oracle(got, ref, keys, Eb, C, vq.tie_counter.value(), f"blockvq nb=8 scale {scale:g}")
+
+
 def test_blockvq_encode_exact_ties(dev):
     """Constructed ties: duplicated centroids (exactly equal distances, the
     first index wins), keys shaped onto midpoints of two centroids (distances

@@ -12,6 +12,9 @@ workloads in seconds):
 c3: 32 sequences x 32768 tokens x 8 KV heads (3-bit scalar keys, bf16).
 c2: 16 x 32768 x 8 token-heads, block-VQ (8-dim blocks, 256 centroids).
 c5: 256 paged sequences, lengths U[1024, 16384], 16-token blocks.
+c4: 2048 causal queries (28 heads) over 65408 block-VQ history tokens
+    (block_dim 2) + 128 fp16 recent tokens; sampled query tokens against the
+    oracle run on those queries alone.
 """
 
 from __future__ import annotations
@@ -143,3 +146,36 @@ def test_c5_full_size_paged(dev):
                            R.ValueQ(gather(vd), gather(vsc), gather(vz), 2), L)
         ref_o = R.hybrid_attention(q[b:b + 1].cpu(), _FlatStore(flat, codec, D, Hkv), None, None, Hq)
         assert_attn_close(out[b:b + 1], ref_o, f"c5 full size, sequence {b} ({L} tokens)")
+
+
+def test_c4_full_size_prefill(dev):
+    Hq, Hkv, D = 28, 4, 128
+    N, Rn, T = 65536 - 128, 128, 2048
+    g = torch.Generator().manual_seed(3)
+    outl = torch.randperm(D, generator=g)[:4]
+    calib_k = sample_keys(4096, seed=31)
+    calib_k[:, outl] *= 20
+    calib_q = sample_keys(4096, seed=32)
+    strat = S.SMAQBlockVQStrategy(D, block_dim=2, n_centroids=256, device=dev)
+    strat.quantizer.fit(calib_k.to(dev), calib_q.to(dev), kmeans_iters=3, on_device=True)
+    keys = dev_sample_keys(N * Hkv, seed=33, device=dev, dtype=torch.float16).view(N, Hkv, D)
+    keys[..., outl.to(dev)] *= 20
+    vals = dev_sample_values(N * Hkv, seed=34, device=dev, dtype=torch.float16).view(N, Hkv, D)
+    st = S.CompressedKVStore(D, Hkv, device=dev, key_strategy=strat)
+    st.append_chunk(keys, vals)
+    kr = dev_sample_keys(Rn * Hkv, seed=35, device=dev, dtype=torch.float16).view(Rn, Hkv, D)
+    kr[..., outl.to(dev)] *= 20
+    vr = dev_sample_values(Rn * Hkv, seed=36, device=dev, dtype=torch.float16).view(Rn, Hkv, D)
+    q = dev_sample_keys(T * Hq, seed=37, device=dev, dtype=torch.float16).view(T, Hq, D)
+    pos = torch.arange(N + Rn - T, N + Rn, device=dev)
+    out = S.compute_hybrid_attention(q, st, kr, vr, Hq, query_positions=pos).cpu()
+    qz = strat.quantizer
+    codec = R.BlockVQCodec(qz.E_blocks.cpu(), qz.centroids.cpu(), qz.decoded_centroids.cpu())
+    gf = st.get_flat_cache()
+    flat = R.FlatCache(R.BlockQ(gf.key_q.indices.cpu(), gf.key_q.n_blocks, gf.key_q.block_dim),
+                       R.ValueQ(gf.value_q.data.cpu(), gf.value_q.scales.cpu(), gf.value_q.zeros.cpu(),
+                                gf.value_q.bits), gf.num_tokens)
+    ost = _FlatStore(flat, codec, D, Hkv)
+    for sl in (slice(0, 16), slice(T - 16, T)):
+        ref_o = R.hybrid_attention(q[sl].cpu(), ost, kr.cpu(), vr.cpu(), Hq, query_positions=pos[sl].cpu())
+        assert_attn_close(out[sl], ref_o, f"c4 full size, queries {sl.start}..{sl.stop - 1}")

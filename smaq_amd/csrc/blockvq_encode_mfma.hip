@@ -179,22 +179,24 @@ __global__ __launch_bounds__(kVmThreads) void encode_blockvq_mfma_kernel(
       const float* cc = C + ((int64_t)b * kVmNc + c) * kVmBd;
       float s = 0.0f;
       for (int e = 0; e < kVmBd; ++e) {
-        amax = fmaxf(amax, fabsf(cc[e]));
+        amax = __builtin_elementwise_maximum(amax, fabsf(cc[e]));  // a NaN is kept
         s = s + cc[e] * cc[e];
       }
       smax = fmaxf(smax, s);
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
-      amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+      amax = __builtin_elementwise_maximum(amax, __shfl_xor(amax, off, 64));
       smax = fmaxf(smax, __shfl_xor(smax, off, 64));
     }
     if (lane == 0) {
+      // a block with a non-finite centroid (the reference's argmin then
+      // follows NaN distances) or outside a sane range sends every token to
+      // the exact path: a NaN sigma makes every distance NaN
+      const bool finite = amax < 3.0e38f;  // false for inf and NaN
       int e = 0;
-      if (amax > 0.0f && amax < 3.0e38f) frexpf(amax, &e);  // amax in [2^(e-1), 2^e)
-      // a codebook outside a sane range (or non-finite) sends every token to
-      // the exact path (NaN sigma makes every distance NaN)
-      sig_all[b] = (e > -100 && e < 100) ? ldexpf(1.0f, 12 - e) : __builtin_nanf("");
+      if (finite && amax > 0.0f) frexpf(amax, &e);  // amax in [2^(e-1), 2^e)
+      sig_all[b] = (finite && e > -100 && e < 100) ? ldexpf(1.0f, 12 - e) : __builtin_nanf("");
       smax_all[b] = smax;
     }
   }
@@ -206,8 +208,7 @@ __global__ __launch_bounds__(kVmThreads) void encode_blockvq_mfma_kernel(
   __syncthreads();
   // ---- split codebook: ch / cl rows of sigma C, q = |sigma C|^2 / 2^14 split
   for (int i = tid; i < L.nq() * 4 * kVmNc; i += kVmThreads) {
-    const int c = i % kVmNc, jb = i / kVmNc;  // jb = 4 * (b / 4) + b % 4
-    const int b = jb;
+    const int c = i % kVmNc, b = i / kVmNc;  // q row b / 4, dword b % 4
     uint32_t qw = 0u;
     if (b < nb) {
       const float sg = sig_all[b];
@@ -217,12 +218,12 @@ __global__ __launch_bounds__(kVmThreads) void encode_blockvq_mfma_kernel(
       uint32_t hw[4], lw[4];
       float q = 0.0f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float v0 = cc[i] * sg, v1 = cc[i + 4] * sg;
+      for (int d = 0; d < 4; ++d) {
+        const float v0 = cc[d] * sg, v1 = cc[d + 4] * sg;
         const _Float16 h0 = (_Float16)v0, h1 = (_Float16)v1;
         const _Float16 l0 = (_Float16)(v0 - (float)h0), l1 = (_Float16)(v1 - (float)h1);
-        hw[i] = h16(h0) | (h16(h1) << 16);
-        lw[i] = h16(l0) | (h16(l1) << 16);
+        hw[d] = h16(h0) | (h16(h1) << 16);
+        lw[d] = h16(l0) | (h16(l1) << 16);
         q = fmaf(v0, v0, q);
         q = fmaf(v1, v1, q);
       }
@@ -232,7 +233,7 @@ __global__ __launch_bounds__(kVmThreads) void encode_blockvq_mfma_kernel(
       const _Float16 qh = (_Float16)qs, ql = (_Float16)(qs - (float)qh);
       qw = sg == sg ? (h16(qh) | (h16(ql) << 16)) : 0u;
     }
-    ((uint32_t*)(lds + L.cq()))[((size_t)(jb >> 2) * kVmNc + c) * 4 + (jb & 3)] = qw;
+    ((uint32_t*)(lds + L.cq()))[((size_t)(b >> 2) * kVmNc + c) * 4 + (b & 3)] = qw;
   }
   __syncthreads();
 

@@ -303,6 +303,27 @@ def test_blockvq_encode_matrix_core_ranges(dev, scale):
     _check_vq_against_oracle(got, ref, keys, Eb, C, vq.tie_counter.value(), f"blockvq nb=8 scale {scale:g}")
 
 
+def test_blockvq_encode_nonfinite_codebook(dev):
+    """A NaN or infinite centroid component: the reference's cdist gives NaN
+    distances and its argmin returns the first NaN's index (every key of the
+    NaN block; the keys whose shaped component meets the infinity with the
+    opposite sign); the matrix-core encoder sends such blocks to its exact
+    recount and must return the same indices."""
+    Eb, Eib, C, Dc = _vq_setup(seed=6)
+    C = C.clone()
+    C[3, 17, 2] = float("nan")
+    C[5, 40, 0] = float("inf")
+    vq = S.SMAQBlockVQ(128, block_dim=8, device=dev)
+    vq.E_blocks, vq.E_inv_blocks = Eb.to(dev), Eib.to(dev)
+    vq.centroids, vq.decoded_centroids = C.to(dev), Dc.to(dev)
+    keys = sample_keys(2000, seed=92)
+    ref = R.blockvq_encode(keys, Eb, C).indices
+    got = vq.quantize(keys.to(dev)).indices.cpu().long()
+    assert bool((ref[:, 3] == 17).all()) and bool((ref[:, 5] == 40).any())
+    assert torch.equal(got[:, 3], ref[:, 3]) and torch.equal(got[:, 5], ref[:, 5])
+    _check_vq_against_oracle(got, ref, keys, Eb, C, 2 ** 31, "blockvq non-finite codebook")
+
+
 def test_blockvq_encode_exact_ties(dev):
     """Constructed ties: duplicated centroids (exactly equal distances, the
     first index wins), keys shaped onto midpoints of two centroids (distances

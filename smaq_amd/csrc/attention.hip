@@ -328,19 +328,40 @@ __global__ __launch_bounds__(kMaxHeadDim) void attn_combine_kernel(smaq_attn_par
   const int d = threadIdx.x;
   if (d >= D) return;
   const int64_t base = part.idx(b, h, p.n_kv_heads, rows, r, 0);
+  // splits in chunks of 8 whose loads are all issued before any is used (one
+  // memory round trip per chunk); a later chunk with a larger maximum rescales
+  // the sums.  With up to 8 splits this is the plain two-pass merge.
   float M = -__builtin_inff();
-#pragma unroll 8
-  for (int s = 0; s < part.S; ++s)
-    if (part.l[base + s] > 0.0f) M = fmaxf(M, part.m[base + s]);
   float L = 0.0f, oh = 0.0f, orc = 0.0f;
-#pragma unroll 8
-  for (int s = 0; s < part.S; ++s) {
-    const float l = part.l[base + s];
-    if (!(l > 0.0f)) continue;
-    const float w = __expf(part.m[base + s] - M);
-    L = fmaf(l, w, L);
-    const float v = part.o[(base + s) * D + d] * w;
-    if (s < s_hist) oh += v; else orc += v;
+  for (int s0 = 0; s0 < part.S; s0 += 8) {
+    float mv[8], lv[8], ov[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int s = min(s0 + i, part.S - 1);
+      lv[i] = part.l[base + s];
+      mv[i] = part.m[base + s];
+      ov[i] = part.o[(base + s) * D + d];
+      if (s0 + i >= part.S) lv[i] = 0.0f;
+    }
+    float Mc = M;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (lv[i] > 0.0f) Mc = fmaxf(Mc, mv[i]);
+    if (Mc > M) {
+      const float c = __expf(M - Mc);
+      L *= c;
+      oh *= c;
+      orc *= c;
+      M = Mc;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (!(lv[i] > 0.0f)) continue;
+      const float w = __expf(mv[i] - M);
+      L = fmaf(lv[i], w, L);
+      const float v = ov[i] * w;
+      if (s0 + i < s_hist) oh += v; else orc += v;
+    }
   }
   const float inv = L > 0.0f ? 1.0f / L : 0.0f;
   oh *= inv;

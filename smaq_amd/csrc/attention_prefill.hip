@@ -119,7 +119,11 @@ __device__ __forceinline__ void store_values(_Float16* img, const float (*vs)[kK
   }
 }
 
-template <int KEY, typename TN, typename TV>
+// WIDE: the thread's 32 dims are 16 key bytes (two codes or two 2-dim block
+// indices per byte, 64-byte key rows) and 8 value bytes (2-bit codes, groups
+// of 32, 32-byte value rows) with one scale / zero, read as one 16-byte and
+// one 8-byte load; the decoded numbers are the same as the byte-wise path's.
+template <int KEY, typename TN, typename TV, bool WIDE>
 __global__ __launch_bounds__(256) void decode_hist_planes_kernel(smaq_attn_params p, HistAddr addr,
                                                                  PrefillPlanes pl) {
   __shared__ float vs[kD][kKT + 1];
@@ -131,7 +135,39 @@ __global__ __launch_bounds__(256) void decode_hist_planes_kernel(smaq_attn_param
   const int64_t len = p.hist_len ? min((int64_t)p.hist_len[b], (int64_t)p.max_hist_len) : p.max_hist_len;
   _Float16* img = pl.img + (((int64_t)b * p.n_kv_heads + h) * (pl.Lp / kKT) + blockIdx.x) * kImg;
   float kv[32];
-  if (t < len) {
+  if (WIDE && t < len) {
+    const int64_t ra = addr.row(b, h, t);
+    const uint4 kb = *(const uint4*)((const uint8_t*)p.key_bytes + ra * 64 + dq / 2);
+    const uint32_t kw[4] = {kb.x, kb.y, kb.z, kb.w};
+    if constexpr (KEY == SMAQ_KEY_SCALAR) {
+      const float nrm = Num<TN>::to_f(((const TN*)p.key_norms)[ra]);
+      const int kbits = p.key_bits;
+      const uint32_t kmask = (1u << kbits) - 1u;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const uint32_t byte = (kw[j >> 2] >> (8 * (j & 3))) & 0xffu;
+        kv[2 * j] = p.key_lut[byte & kmask] * nrm;
+        kv[2 * j + 1] = p.key_lut[(byte >> kbits) & kmask] * nrm;
+      }
+    } else {
+      const int nc = p.vq_centroids;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int ci = min((int)((kw[j >> 2] >> (8 * (j & 3))) & 0xffu), nc - 1);
+        const float2 c = *(const float2*)(p.key_lut + ((int64_t)(dq / 2 + j) * nc + ci) * 2);
+        kv[2 * j] = c.x;
+        kv[2 * j + 1] = c.y;
+      }
+    }
+    const uint2 vb = *(const uint2*)((const uint8_t*)p.val_bytes + ra * 32 + dq / 4);
+    const float sc = Num<TV>::to_f(((const TV*)p.val_scales)[ra * 4 + (tid & 3)]);
+    const float z = Num<TV>::to_f(((const TV*)p.val_zeros)[ra * 4 + (tid & 3)]);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const uint32_t code = ((i < 16 ? vb.x : vb.y) >> (2 * (i & 15))) & 3u;
+      vs[dq + i][tt] = (float)code * sc + z;
+    }
+  } else if (t < len) {
     const int64_t ra = addr.row(b, h, t);
     const uint8_t* kr = (const uint8_t*)p.key_bytes + ra * p.key_row_bytes;
     float nrm = 1.0f;
@@ -488,11 +524,20 @@ int64_t prefill_split_len(const smaq_attn_params& p, int64_t L) {
 int launch_prefill_planes_hist(const smaq_attn_params& p, const HistAddr& a, const PrefillPlanes& pl,
                                hipStream_t st) {
   dim3 grid((unsigned)(pl.Lp / kKT), p.n_kv_heads, p.batch);
-#define SMAQ_PLANES_V(KEY, TN)                                                                        \
-  switch (p.val_dtype) {                                                                              \
-    case SMAQ_F32: hipLaunchKernelGGL((decode_hist_planes_kernel<KEY, TN, float>), grid, dim3(256), 0, st, p, a, pl); break; \
-    case SMAQ_F16: hipLaunchKernelGGL((decode_hist_planes_kernel<KEY, TN, _Float16>), grid, dim3(256), 0, st, p, a, pl); break; \
-    default: hipLaunchKernelGGL((decode_hist_planes_kernel<KEY, TN, bf16>), grid, dim3(256), 0, st, p, a, pl); break; \
+  const bool wide_keys = p.key_row_bytes == 64 && ((uintptr_t)p.key_bytes & 15) == 0 &&
+                         (p.key_format == SMAQ_KEY_SCALAR ? (p.key_bits == 3 || p.key_bits == 4)
+                                                          : (p.vq_block_dim == 2 && p.vq_centroids <= 256 &&
+                                                             ((uintptr_t)p.key_lut & 7) == 0));
+  const bool wide = wide_keys && p.val_bits == 2 && p.val_group == 32 && p.val_row_bytes == 32 &&
+                    ((uintptr_t)p.val_bytes & 7) == 0;
+#define SMAQ_PLANES_W(KEY, TN, TV)                                                                          \
+  if (wide) hipLaunchKernelGGL((decode_hist_planes_kernel<KEY, TN, TV, true>), grid, dim3(256), 0, st, p, a, pl); \
+  else hipLaunchKernelGGL((decode_hist_planes_kernel<KEY, TN, TV, false>), grid, dim3(256), 0, st, p, a, pl);
+#define SMAQ_PLANES_V(KEY, TN)                             \
+  switch (p.val_dtype) {                                   \
+    case SMAQ_F32: SMAQ_PLANES_W(KEY, TN, float); break;    \
+    case SMAQ_F16: SMAQ_PLANES_W(KEY, TN, _Float16); break; \
+    default: SMAQ_PLANES_W(KEY, TN, bf16); break;           \
   }
   if (p.key_format == SMAQ_KEY_SCALAR) {
     switch (p.norm_dtype) {
@@ -504,6 +549,7 @@ int launch_prefill_planes_hist(const smaq_attn_params& p, const HistAddr& a, con
     SMAQ_PLANES_V(SMAQ_KEY_BLOCKVQ, float);
   }
 #undef SMAQ_PLANES_V
+#undef SMAQ_PLANES_W
   return launch_status("smaq_attn_hybrid(prefill planes)");
 }
 

@@ -72,6 +72,30 @@ def test_prefill_blockvq_vs_oracle(dev):
     assert_attn_close(out, R.hybrid_attention(q, ref, kr, vr, hq, query_positions=pos), "prefill block-VQ")
 
 
+def test_prefill_bytewise_decode_vs_oracle(dev):
+    """Formats the tile pre-pass decodes byte by byte (8-dim VQ blocks, 4-bit
+    values in groups of 16; the 2-dim / 2-bit formats above take its
+    16-byte loads): 300 history tokens, no recent window, 70 causal queries."""
+    hkv, hq, N, T = 2, 4, 300, 70
+    keys = sample_keys(N * hkv, seed=218).reshape(N, hkv, 128)
+    vals = torch.randn(N, hkv, 128, generator=torch.Generator().manual_seed(219))
+    strat = S.SMAQBlockVQStrategy(128, block_dim=8, n_centroids=256, device=dev)
+    strat.quantizer.fit(sample_keys(2048, seed=220), sample_keys(2048, seed=221), kmeans_iters=3)
+    qz = strat.quantizer
+    codec = R.BlockVQCodec(qz.E_blocks.cpu(), qz.centroids.cpu(), qz.decoded_centroids.cpu())
+    st = S.CompressedKVStore(128, hkv, value_bits=4, value_group_size=16, device=dev, key_strategy=strat)
+    ref = R.Store(codec, 128, hkv, value_bits=4, value_group_size=16)
+    st.append_chunk(keys.half().to(dev), vals.half().to(dev))
+    ref.append_chunk(keys.half(), vals.half())
+    got_idx = st.get_flat_cache().key_q.indices.cpu().long()
+    if not torch.equal(got_idx, ref.get_flat_cache().key_q.indices):
+        ref.kc = [R.BlockQ(got_idx.unsqueeze(0), 16, 8)]   # score the same codes on both sides
+    q = sample_keys(T * hq, seed=222).reshape(T, hq, 128).half()
+    pos = torch.arange(N - T, N)
+    out = S.compute_hybrid_attention(q.to(dev), st, None, None, hq, query_positions=pos.to(dev), impl=3)
+    assert_attn_close(out, R.hybrid_attention(q, ref, None, None, hq, query_positions=pos), "prefill byte-wise")
+
+
 def test_prefill_large_vs_generic(dev):
     """Qwen2-7B head shape (28/4) at 20000 history tokens and 300 causal
     queries: matrix-core prefill against the generic kernels."""

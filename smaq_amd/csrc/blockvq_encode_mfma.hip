@@ -30,8 +30,8 @@
 // encodes 16 tokens at a time, block after block, with the next block's key
 // bytes in flight.  The running minimum keeps the distance bits with the low
 // 6 bits replaced by the centroid's position in the lane (tile, row), so one
-// v_min_u32 tracks value and index (distances are positive: delta is added to
-// every one) and one v_med3_u32 the runner-up.
+// v_min3_u32 tracks value and index of two distances (distances are positive:
+// delta is added to every one) and a v_med3_u32 / v_min_u32 pair the runner-up.
 #include "encode_internal.h"
 
 namespace smaq {
@@ -69,11 +69,18 @@ __device__ __forceinline__ uint32_t fbits(float x) { return __builtin_bit_cast(u
 __device__ __forceinline__ float bitsf(uint32_t b) { return __builtin_bit_cast(float, b); }
 __device__ __forceinline__ uint32_t h16(_Float16 h) { return (uint32_t)__builtin_bit_cast(uint16_t, h); }
 
-// Middle of three (v_med3_u32): with best <= second, med3(best, second, key)
-// is the new runner-up after `key`.
+// Two keys k0, k1 at a time: with best <= second, the new minimum is
+// min3(best, k0, k1) and the new runner-up min(second, med3(best, k0, k1))
+// (the overall minimum lies in {best, k0, k1}, so the second smallest of the
+// four is the smaller of `second` and the middle of those three).
 __device__ __forceinline__ uint32_t med3_u32(uint32_t a, uint32_t b, uint32_t c) {
   uint32_t r;
   asm("v_med3_u32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ __forceinline__ uint32_t min3_u32(uint32_t a, uint32_t b, uint32_t c) {
+  uint32_t r;
+  asm("v_min3_u32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
   return r;
 }
 
@@ -316,11 +323,12 @@ __global__ __launch_bounds__(kVmThreads) void encode_blockvq_mfma_kernel(
         if (t + 1 < 16)
           acc_next = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, ap[16 * (t + 1)]), bv, acc0, 0, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          // centroid 16t + 4kg + i of token n; low 6 bits = (t, i)
-          const uint32_t key = (fbits(acc[i]) & 0xffffffc0u) | (uint32_t)(4 * t + i);
-          second = med3_u32(best, second, key);
-          best = min(best, key);
+        for (int i = 0; i < 4; i += 2) {
+          // centroids 16t + 4kg + i, i + 1 of token n; low 6 bits = (t, i)
+          const uint32_t k0 = (fbits(acc[i]) & 0xffffffc0u) | (uint32_t)(4 * t + i);
+          const uint32_t k1 = (fbits(acc[i + 1]) & 0xffffffc0u) | (uint32_t)(4 * t + i + 1);
+          second = min(second, med3_u32(best, k0, k1));
+          best = min3_u32(best, k0, k1);
         }
       }
       // merge the four k-group lanes of each token

@@ -51,6 +51,22 @@ def test_mfma_decode_contiguous(dev, bits, g, dtype):
         assert_attn_close(out_g[b:b + 1], ref, f"generic {bits}b g={g} seq {b}")
 
 
+def test_mfma_decode_many_splits(dev):
+    """One sequence, 2 KV heads, 20000 tokens: the context is cut into 40
+    splits of 512 tokens, so the split merge runs five chunks of loads and
+    rescales its sums whenever a later chunk holds a larger maximum."""
+    strat, codec = _codec_pair(dev, 3, 280)
+    hkv, g, n = 2, 4, 20000
+    keys = sample_keys(n * hkv, seed=281).reshape(n, hkv, 128).bfloat16()
+    vals = torch.randn(n, hkv, 128, generator=torch.Generator().manual_seed(282)).bfloat16()
+    # a late token the queries align with, so the maximum moves in a late chunk
+    keys[18000] = keys[18000] * 4
+    kvb = QuantizedKVBatch.encode(strat, [keys.to(dev)], [vals.to(dev)])
+    q = keys[18000].float().repeat_interleave(g, dim=0).unsqueeze(0).bfloat16()
+    out = kvb.attention(q.to(dev), impl=2)
+    assert_attn_close(out, _oracle(codec, keys, vals, q, hkv * g, hkv), "mfma 40 splits")
+
+
 def test_mfma_decode_paged(dev):
     strat, codec = _codec_pair(dev, 3, 260)
     gen = torch.Generator().manual_seed(261)

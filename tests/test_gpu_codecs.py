@@ -190,18 +190,19 @@ def test_scalar_dequant_scores_rotate(dev):
 @pytest.mark.parametrize("scaled", [False, True])
 def test_rotate_rows_128_chunking_and_accuracy(dev, dtype, scaled):
     """smaq_rotate_rows at head_dim 128 (the decode query rotation): one
-    sequential fmaf chain per output, so 5000 rows in one call equal the same
-    rows in two calls of 2500 bit for bit, and match the float64 product
-    within the rounding bound of a 128-term fp32 chain."""
+    sequential fmaf chain per output, so 5001 rows in one call (8-row blocks,
+    the last one partial) equal the same rows in two calls of 2500 and 2501
+    (2-row blocks) bit for bit, and match the float64 product within the
+    rounding bound of a 128-term fp32 chain."""
     g = torch.Generator().manual_seed(130)
     M = torch.linalg.qr(torch.randn(128, 128, generator=g, dtype=torch.float64))[0].float()
     cs = (torch.rand(128, generator=g) + 0.5) if scaled else None
-    x = torch.randn(5000, 128, generator=g).to(dtype)
+    x = torch.randn(5001, 128, generator=g).to(dtype)
     Mt, csd = M.T.contiguous().to(dev), None if cs is None else cs.to(dev)
     xd = x.to(dev)
-    whole = torch.empty(5000, 128, device=dev)
+    whole = torch.empty(5001, 128, device=dev)
     _native.rotate_rows_into(xd, Mt, csd, whole)
-    parts = torch.empty(5000, 128, device=dev)
+    parts = torch.empty(5001, 128, device=dev)
     _native.rotate_rows_into(xd[:2500], Mt, csd, parts[:2500])
     _native.rotate_rows_into(xd[2500:], Mt, csd, parts[2500:])
     assert torch.equal(whole, parts)

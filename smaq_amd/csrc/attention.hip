@@ -337,11 +337,14 @@ __global__ __launch_bounds__(kMaxHeadDim) void attn_combine_kernel(smaq_attn_par
     float mv[8], lv[8], ov[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int s = min(s0 + i, part.S - 1);
-      lv[i] = part.l[base + s];
-      mv[i] = part.m[base + s];
-      ov[i] = part.o[(base + s) * D + d];
-      if (s0 + i >= part.S) lv[i] = 0.0f;
+      lv[i] = 0.0f;
+      mv[i] = -__builtin_inff();
+      ov[i] = 0.0f;
+      if (s0 + i < part.S) {  // uniform: loads of splits that exist only
+        lv[i] = part.l[base + s0 + i];
+        mv[i] = part.m[base + s0 + i];
+        ov[i] = part.o[(base + s0 + i) * D + d];
+      }
     }
     float Mc = M;
 #pragma unroll

@@ -316,17 +316,21 @@ __global__ __launch_bounds__(kAttnThreads) void attn_recent_kernel(smaq_attn_par
 }
 
 // ------------------------------------------------------------ combine ------
+// kCombineRows query rows per workgroup (threadIdx.y), one thread per
+// output dim (threadIdx.x): fewer, larger workgroups than one per row
+constexpr int kCombineRows = 4;
+
 template <typename TO>
-__global__ __launch_bounds__(kMaxHeadDim) void attn_combine_kernel(smaq_attn_params p, Partials part,
-                                                                   int s_hist) {
+__global__ __launch_bounds__(kMaxHeadDim * kCombineRows) void attn_combine_kernel(smaq_attn_params p,
+                                                                                  Partials part, int s_hist) {
   const int D = p.head_dim;
   const int g = p.n_q_heads / p.n_kv_heads;
   const int rows = p.q_len * g;
-  const int r = blockIdx.x;   // row within the KV head group
+  const int r = blockIdx.x * kCombineRows + threadIdx.y;  // row within the KV head group
   const int h = blockIdx.y;
   const int b = blockIdx.z;
   const int d = threadIdx.x;
-  if (d >= D) return;
+  if (d >= D || r >= rows) return;
   const int64_t base = part.idx(b, h, p.n_kv_heads, rows, r, 0);
   // splits in chunks of 8 whose loads are all issued before any is used (one
   // memory round trip per chunk); a later chunk with a larger maximum rescales
@@ -592,8 +596,8 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
     if (rc != SMAQ_OK) return rc;
   }
   if (!(phases & 4)) return SMAQ_OK;
-  dim3 cgrid((unsigned)rows, p.n_kv_heads, p.batch);
-  const dim3 cblock((unsigned)((p.head_dim + 63) / 64 * 64));  // one thread per output dim
+  dim3 cgrid((unsigned)((rows + kCombineRows - 1) / kCombineRows), p.n_kv_heads, p.batch);
+  const dim3 cblock((unsigned)((p.head_dim + 63) / 64 * 64), kCombineRows);  // one thread per output dim
   switch (p.out_dtype) {
     case SMAQ_F32: hipLaunchKernelGGL(attn_combine_kernel<float>, cgrid, cblock, 0, st, p, part, pl.s_hist); break;
     case SMAQ_F16: hipLaunchKernelGGL(attn_combine_kernel<_Float16>, cgrid, cblock, 0, st, p, part, pl.s_hist); break;

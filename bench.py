@@ -566,7 +566,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path "
-              "(the hot path shards by sequence/KV head with no exchange; see DESIGN.md). "
+              "(the hot path would shard by sequence / KV head, each GPU attending over its own "
+              "sequences and heads with no exchange). "
               "Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():

@@ -28,6 +28,16 @@ PINNING -- what checks each function (tests/test_oracle_*.py):
   ordering and symmetry invariants.
 * build_metric / ssf_log: diagonal-Sigma closed form, E @ E_inv = I,
   det(E) = 1 (volume normalisation), symmetry of E^2 eigenvalues.
+* fit_sigma_centered: numpy's biased covariance (np.cov bias=True) with a
+  mean offset that the uncentred and the N-1 forms visibly miss; one- and
+  two-row closed forms; shift invariance.
+* smaq_dequantize: E (k_hat / n) = c[code] with codes from a bit loop (E in
+  place of E_inv fails by orders of magnitude); identity metric bit-exact
+  c[code] * n; diagonal metric closed form.
+* smaq_scores: diagonal-metric float64 loop; q . (n E^-1 c[code]) * scale
+  with E^-1 from a float64 solve of the encoder metric; query dtype output.
+* blockvq_scores: float64 per-block gather loop (16x8, 64x2, 4x32 blocks),
+  flipped block order fails; keys on codewords give the plain dot product.
 * scalar_encode: codes equal a float64 numpy recomputation except where y is
   within 1e-6 (relative) of a decision boundary; norms within 1 ulp of fp64;
   zero key, unit-basis keys, saturation special cases.

@@ -27,6 +27,21 @@ from smaq_amd.store import CompressedKVStore, FlatCache
 MIN_HISTORY_FOR_SMAQ = 16
 
 
+def _per_sequence_index(t: Optional[torch.Tensor], batch: int, dev: torch.device, what: str):
+    """A per-sequence length/start tensor as the kernels read it: int64,
+    contiguous, on the attention's device, one entry per sequence.  Callers
+    hand in vLLM's int32 ``seq_lens`` or host tensors; both are converted here
+    (the kernel dereferences the raw pointer as ``const long long*``)."""
+    if t is None:
+        return None
+    if t.dtype.is_floating_point or t.dtype == torch.bool or t.dtype.is_complex:
+        raise ValueError(f"{what} must be an integer tensor, got {t.dtype}")
+    t = t.reshape(-1)
+    if t.numel() < batch:
+        raise ValueError(f"{what} has {t.numel()} entries for {batch} sequences")
+    return t[:batch].to(dev, torch.int64).contiguous()
+
+
 class AttentionPlan:
     """A prepared fused-attention launch.
 
@@ -83,6 +98,8 @@ class AttentionPlan:
         self.q_exact = torch.empty(B, T, Hq, D, dtype=torch.float32, device=dev)
         p.q_exact = self.q_exact.data_ptr()
         if query_positions is not None:
+            if query_positions.numel() != B * T or query_positions.dtype.is_floating_point:
+                raise ValueError(f"query_positions must be {B * T} integer positions ([batch, q_len])")
             qp = query_positions.to(dev, torch.int64).contiguous()
             keep.append(qp)
             p.q_positions = qp.data_ptr()
@@ -118,11 +135,16 @@ class AttentionPlan:
             p.val_bits, p.val_group = val_bits, val_group
             p.val_scales, p.val_zeros = val_scales.data_ptr(), val_zeros.data_ptr()
             p.val_dtype = _native.dtype_code(val_scales.dtype)
+            hist_len = _per_sequence_index(hist_len, B, dev, "hist_len")
+            hist_seq_start = _per_sequence_index(hist_seq_start, B, dev, "hist_seq_start")
             p.hist_len = None if hist_len is None else hist_len.data_ptr()
             p.hist_seq_start = None if hist_seq_start is None else hist_seq_start.data_ptr()
             p.hist_head_stride = int(hist_head_stride)
             if block_table is not None:
-                bt = block_table.to(dev, torch.int32).contiguous()
+                if block_table.dim() != 2 or block_table.shape[0] < B or block_table.dtype.is_floating_point:
+                    raise ValueError(f"block_table must be an integer [>= {B}, max_blocks] tensor, "
+                                     f"got {tuple(block_table.shape)} {block_table.dtype}")
+                bt = block_table[:B].to(dev, torch.int32).contiguous()
                 keep.append(bt)
                 p.block_table = bt.data_ptr()
                 p.max_blocks = bt.shape[-1]
@@ -132,6 +154,7 @@ class AttentionPlan:
                      if t is not None]
         if has_recent:
             rk, rv = recent_k.contiguous(), recent_v.contiguous()
+            recent_len = _per_sequence_index(recent_len, B, dev, "recent_len")
             keep += [rk, rv] + ([recent_len] if recent_len is not None else [])
             p.has_recent = 1
             p.recent_k, p.recent_v = rk.data_ptr(), rv.data_ptr()

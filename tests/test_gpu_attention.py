@@ -187,3 +187,31 @@ def test_paged_decode(dev):
     out = pk.attention(q.to(dev))
     for b in range(len(lens)):
         assert_attn_close(out[b:b + 1], _oracle_single(codec, keys[b], vals[b], q[b:b + 1], 32, 8), f"paged {b}")
+
+
+def test_length_tensors_any_integer_dtype_or_device(dev):
+    """Per-sequence lengths reach the kernels as int64 on the device whatever
+    the caller hands in: int32 (vLLM's seq_lens) and host tensors give the
+    same output as device int64, bit for bit."""
+    calib = sample_keys(64, seed=170)
+    strat = S.SMAQFullMetricScalarStrategy(128, bits=3, device=dev).fit(calib)
+    lens = [200, 90, 333]
+    keys = [sample_keys(n * 8, seed=171 + i).reshape(n, 8, 128).bfloat16().to(dev) for i, n in enumerate(lens)]
+    vals = [torch.randn(n, 8, 128, generator=torch.Generator().manual_seed(175 + i)).bfloat16().to(dev)
+            for i, n in enumerate(lens)]
+    kvb = QuantizedKVBatch.encode(strat, keys, vals)
+    g = torch.Generator().manual_seed(178)
+    q = torch.randn(3, 32, 128, generator=g).bfloat16().to(dev)
+    rk = torch.randn(3, 16, 8, 128, generator=g).bfloat16().to(dev)
+    rv = torch.randn(3, 16, 8, 128, generator=g).bfloat16().to(dev)
+    base = kvb.attention(q, recent_k=rk, recent_v=rv, recent_len=torch.tensor([16, 3, 9], device=dev))
+    for rl in (torch.tensor([16, 3, 9], dtype=torch.int32, device=dev), torch.tensor([16, 3, 9], dtype=torch.int32),
+               torch.tensor([16, 3, 9])):
+        got = kvb.attention(q, recent_k=rk, recent_v=rv, recent_len=rl)
+        assert torch.equal(got, base), f"recent_len {rl.dtype} on {rl.device}"
+    kvb.hist_len = kvb.hist_len.to(torch.int32).cpu()
+    kvb.seq_start = kvb.seq_start.to(torch.int32)
+    got = kvb.attention(q, recent_k=rk, recent_v=rv, recent_len=torch.tensor([16, 3, 9], device=dev))
+    assert torch.equal(got, base), "int32 host hist_len / int32 seq_start"
+    with pytest.raises(ValueError):
+        kvb.attention(q, recent_k=rk, recent_v=rv, recent_len=torch.tensor([16.0, 3.0, 9.0], device=dev))

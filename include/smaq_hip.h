@@ -9,7 +9,8 @@
  *    thread-local message for the last failure on the calling thread.
  *  - The caller allocates every output and workspace (torch does, on the
  *    Python side).  Entry points never allocate, never synchronise the stream,
- *    and keep no mutable global state (re-entrant).
+ *    and keep no mutable global state (re-entrant), except
+ *    smaq_attn_hybrid_noalloc, whose workspace is one built-in array per GPU.
  *  - dtype codes: SMAQ_F32 = 0, SMAQ_F16 = 1, SMAQ_BF16 = 2.
  *  - "rows" inputs are addressed as row r = o * n_inner + i at element offset
  *    o * s_outer + i * s_inner with a contiguous last dim; outputs are dense
@@ -241,6 +242,23 @@ typedef struct smaq_attn_params {
 /* Bytes of workspace smaq_attn_hybrid needs for these parameters. */
 long long smaq_attn_workspace_bytes(const smaq_attn_params* p);
 int smaq_attn_hybrid(const smaq_attn_params* p, void* stream);
+
+/*
+ * Allocation-free smaq_attn_hybrid.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops that forbid hipMalloc).  Same kernels and results as
+ * smaq_attn_hybrid; p->workspace and p->workspace_bytes are ignored and the
+ * workspace is a built-in device array of SMAQ_NOALLOC_SCRATCH_BYTES per GPU,
+ * held until the process ends.  Parameters whose smaq_attn_workspace_bytes
+ * exceeds that size are rejected with SMAQ_EINVAL (decode batches fit; the
+ * matrix-core prefill's tile images generally do not).  Nothing in the array
+ * needs clearing between calls (every partial a call reads it writes first),
+ * but calls that overlap on one GPU -- on two streams, or two threads --
+ * share the array and race.  The first call on a device looks up the array's
+ * address there (hipGetSymbolAddress); no call allocates or frees memory.
+ */
+#define SMAQ_NOALLOC_SCRATCH_BYTES (32ll << 20)
+int smaq_attn_hybrid_noalloc(const smaq_attn_params* p, void* stream);
 
 #ifdef __cplusplus
 }

@@ -80,7 +80,12 @@ _SIGS = {
     "smaq_kmeans_update": (c_int, [c_void_p, c_void_p, c_int, c_ll, c_int, c_int, c_void_p, c_void_p]),
     "smaq_attn_workspace_bytes": (c_ll, [ctypes.POINTER(AttnParams)]),
     "smaq_attn_hybrid": (c_int, [ctypes.POINTER(AttnParams), c_void_p]),
+    "smaq_attn_hybrid_noalloc": (c_int, [ctypes.POINTER(AttnParams), c_void_p]),
 }
+
+# Size of the built-in workspace of smaq_attn_hybrid_noalloc
+# (SMAQ_NOALLOC_SCRATCH_BYTES in include/smaq_hip.h).
+NOALLOC_SCRATCH_BYTES = 32 << 20
 
 EXPORTED = tuple(_SIGS)
 
@@ -394,3 +399,11 @@ def attn_workspace_bytes(p: AttnParams) -> int:
 def attn_hybrid(p: AttnParams, device: torch.device) -> None:
     """Launches the fused attention described by p (workspace already set)."""
     _check(lib().smaq_attn_hybrid(ctypes.byref(p), _stream(device)), "smaq_attn_hybrid")
+
+
+def attn_hybrid_noalloc(p: AttnParams, device: torch.device) -> None:
+    """Launches the fused attention described by p with the library's
+    built-in per-GPU workspace (p.workspace is ignored; nothing is allocated).
+    Raises ValueError when the shapes need more than NOALLOC_SCRATCH_BYTES.
+    Calls that overlap on one GPU share that workspace and race."""
+    _check(lib().smaq_attn_hybrid_noalloc(ctypes.byref(p), _stream(device)), "smaq_attn_hybrid_noalloc")

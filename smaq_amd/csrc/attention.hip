@@ -606,3 +606,77 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
   }
   return launch_status("smaq_attn_hybrid(combine)");
 }
+
+// ------------------------------------------------ allocation-free variant --
+// smaq_attn_hybrid_noalloc runs smaq_attn_hybrid with the workspace taken from
+// a file-scope device array instead of the caller's buffer, for callers that
+// cannot allocate (code under HIP graph capture, serving loops that forbid
+// hipMalloc).  Each GPU holds its own copy of the array for the life of the
+// process; the host reaches it only through the address hipGetSymbolAddress
+// returns on that device (the array's name in host code is not a device
+// address).
+#include <mutex>
+
+namespace smaq {
+
+constexpr long long kNoAllocScratchBytes = SMAQ_NOALLOC_SCRATCH_BYTES;
+constexpr int kNoAllocMaxDevices = 64;
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kNoAllocMaxDevices];
+
+// Device address of `scratch` on the stream's device, looked up once per
+// device with that device current.
+static int scratch_for_stream(hipStream_t st, void** out) {
+  int dev = -1;
+  hipError_t e = hipStreamGetDevice(st, &dev);
+  if (e != hipSuccess) {
+    set_error("smaq_attn_hybrid_noalloc: hipStreamGetDevice failed: %s", hipGetErrorString(e));
+    return SMAQ_ELAUNCH;
+  }
+  SMAQ_REQUIRE(dev >= 0 && dev < kNoAllocMaxDevices, "smaq_attn_hybrid_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    int cur = -1;
+    if ((e = hipGetDevice(&cur)) != hipSuccess) {
+      set_error("smaq_attn_hybrid_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+      return SMAQ_ELAUNCH;
+    }
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) {
+      set_error("smaq_attn_hybrid_noalloc: hipSetDevice(%d) failed: %s", dev, hipGetErrorString(e));
+      return SMAQ_ELAUNCH;
+    }
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (cur != dev) (void)hipSetDevice(cur);
+    if (e != hipSuccess || ptr == nullptr) {
+      set_error("smaq_attn_hybrid_noalloc: hipGetSymbolAddress(scratch) on device %d failed: %s", dev,
+                hipGetErrorString(e));
+      return SMAQ_ELAUNCH;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return SMAQ_OK;
+}
+
+}  // namespace smaq
+
+extern "C" int smaq_attn_hybrid_noalloc(const smaq_attn_params* pp, void* stream) {
+  SMAQ_REQUIRE(pp, "smaq_attn_hybrid_noalloc: null params");
+  const long long need = smaq_attn_workspace_bytes(pp);
+  SMAQ_REQUIRE(need >= 0, "smaq_attn_hybrid_noalloc: invalid parameters");
+  SMAQ_REQUIRE(need <= smaq::kNoAllocScratchBytes,
+               "smaq_attn_hybrid_noalloc: these shapes need %lld bytes of workspace, more than the %lld-byte "
+               "built-in scratch; use smaq_attn_hybrid with a caller workspace",
+               need, smaq::kNoAllocScratchBytes);
+  void* ws = nullptr;
+  const int rc = smaq::scratch_for_stream((hipStream_t)stream, &ws);
+  if (rc != SMAQ_OK) return rc;
+  smaq_attn_params p = *pp;
+  p.workspace = ws;
+  p.workspace_bytes = smaq::kNoAllocScratchBytes;
+  return smaq_attn_hybrid(&p, stream);
+}

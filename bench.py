@@ -1,18 +1,32 @@
 #!/usr/bin/env python
 """SMAQ quantized-KV hot path benchmark on one MI355X.
 
-Default workload: fused quantized-KV decode attention at
-Llama-3-8B shape -- batch 32, context 32768, 32 query / 8 KV heads, head_dim
-128, keys 3-bit scalar SMAQ (calibrated metric), values 2-bit (group 32),
-bf16 queries, one new token per sequence.  One step = one decode-attention
-pass of one layer over the whole batch, cache resident in HBM.
+    python bench.py [--steps K] [--warmup W] [--workload all|decode|paged|prefill|encode]
 
-    python bench.py [--steps K] [--warmup W] [--workload decode|encode|paged]
+Prints ONE JSON line.  The default (``all``) runs the four BASELINE workloads
+back to back on one GPU; the headline fields are config 3, the others are
+records under ``extra``:
 
-Prints ONE JSON line.  ``value`` is decode tokens/s (batch / step time);
-``roofline`` is the dominant kernel (decode_mfma_kernel, history partials) timed with HIP
-events on the launch stream, against its algorithmic bytes (114 B per
-token-head); ``cpu_baseline`` times the CPU oracle on a bounded sample.
+* c3 (headline) fused quantized-KV decode attention at Llama-3-8B shape --
+  batch 32, context 32768, 32 query / 8 KV heads, head_dim 128, 3-bit scalar
+  SMAQ keys (calibrated metric), 2-bit values (group 32), bf16 storage and
+  queries, one new token per sequence.  One step = one decode-attention pass
+  of one layer over the whole batch, cache resident in HBM; ``value`` is
+  tokens/s = batch / step time.
+* c5 paged decode (256 sequences, 16-token blocks, shuffled block tables).
+* c4 hybrid chunked prefill (2048 causal queries over 65408 block-VQ history
+  tokens + 128 exact recent tokens, Qwen2-7B heads).
+* c2 block-VQ key encode + 2-bit value pack of 4.19M bf16 token-heads.
+
+Every workload: a settle phase (back-to-back steps for ``--settle-ms`` of
+wall time: on MI355X the first few ms of a heavy load run inside a
+power-management transient during which this kernel first runs fast, then
+up to 30% slower, before it settles), then W untimed warm-up steps, then K
+timed steps between two HIP events on the launch stream.  ``roofline`` is
+the dominant kernel alone: HIP events on its launch stream (torch's current
+stream) around K back-to-back launches, against its algorithmic bytes or
+flops.  ``cpu_baseline`` times the CPU oracle (the op-for-op torch
+restatement of the reference) on a bounded sample on this host.
 """
 
 from __future__ import annotations
@@ -32,36 +46,152 @@ sys.path.insert(0, ROOT)
 METRIC = "quantized-KV decode attn tokens/s + achieved HBM GB/s (% peak); encode GB/s"
 HBM_PEAK_GBS = 8000.0
 FP32_PEAK_TFLOPS = 157.3
+F16_PEAK_TFLOPS = 2500.0
+
+# What the decode kernels compute in (storage is bf16): QK as three f16
+# products of hi/lo splits (~22-bit scores), PV as two bf16 products of a
+# hi/lo split weight against exact 2-bit codes, fp32 softmax and accumulation.
+DECODE_DTYPE = "bf16 storage; QK 3x f16 hi/lo MFMA (~22-bit), PV 2x bf16 hi/lo MFMA on exact codes, fp32 accumulate"
+PREFILL_DTYPE = "fp16 storage; QK and PV 3x f16 hi/lo MFMA, fp32 accumulate"
+ENCODE_DTYPE = "bf16 in; fp32-exact distances (f16 hi/lo MFMA + exact recount), u8 indices, 2-bit values"
 
 
 def _events(n):
     return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
 
 
-def _cores() -> int:
-    return torch.get_num_threads()
+def cpu_threads() -> int:
+    """Threads the CPU baseline uses: the host's cores as this process may use
+    them (affinity), capped by OMP_NUM_THREADS when the environment sets it
+    (the GPU boxes give one GPU's job a 16-thread share of the host)."""
+    n = os.cpu_count() or 1
+    try:
+        n = min(n, len(os.sched_getaffinity(0)))
+    except AttributeError:
+        pass
+    omp = os.environ.get("OMP_NUM_THREADS")
+    if omp and omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return n
 
 
-def history_kernel_ms(plan, q, steps: int) -> float:
-    """Mean duration of the history-partials kernel alone: HIP events on the
-    plan's launch stream (torch's current stream) around `steps` back-to-back
-    launches of that phase (the query is loaded once; every launch recomputes
-    the same partials), so no host-side gap between launches is timed."""
-    plan.load_query(q)
-    plan.launch(phases=1)
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _cpu_fields() -> dict:
+    return {"cores": torch.get_num_threads(), "cpu_model": cpu_model(), "cpu_count": os.cpu_count()}
+
+
+def settle(step, ms: float) -> dict:
+    """Back-to-back steps for `ms` of wall time (synchronising every 16), so
+    the timed steps run at the GPU's steady clocks."""
+    n = 0
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(16):
+            step()
+        n += 16
+        torch.cuda.synchronize()
+    return {"ms": round((time.perf_counter() - t0) * 1e3, 1), "steps": n}
+
+
+def time_steps(step, args) -> tuple[float, dict]:
+    """Settle, W warm-up steps, then the mean time of K steps (ms)."""
+    st = settle(step, args.settle_ms) if args.settle_ms > 0 else {"ms": 0.0, "steps": 0}
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    start, end = _events(2)
+    start.record()
+    for _ in range(args.steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / args.steps, st
+
+
+def kernel_ms(launch, steps: int) -> float:
+    """Mean duration of `launch` alone: HIP events on the launch stream
+    (torch's current stream) around `steps` back-to-back launches."""
+    launch()
     a, b = _events(2)
     a.record()
     for _ in range(steps):
-        plan.launch(phases=1)
+        launch()
     b.record()
     torch.cuda.synchronize()
     return a.elapsed_time(b) / steps
 
 
+def _median_time(fn, reps: int = 3) -> float:
+    fn()  # warm-up
+    times = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+    return statistics.median(times)
+
+
+def recorded_traffic(name: str, config: dict):
+    """HBM bytes per launch of the dominant kernel, as measured by the
+    rocprofv3 FETCH_SIZE / WRITE_SIZE passes recorded in profiles/<name>.md
+    (line ``traffic_bytes_per_launch = N``, with the config it was taken on).
+    None when no record matches this configuration."""
+    path = os.path.join(ROOT, "profiles", name + ".md")
+    if not os.path.exists(path):
+        return None
+    rec = {}
+    with open(path) as f:
+        for line in f:
+            if "=" in line and line.strip().startswith(("traffic_bytes_per_launch", *config)):
+                k, v = line.split("=", 1)
+                rec[k.strip()] = int(v.strip())
+    if "traffic_bytes_per_launch" not in rec or any(rec.get(k) != v for k, v in config.items()):
+        return None
+    return rec["traffic_bytes_per_launch"]
+
+
+def _record(args, *, value, unit, ms_step, dtype, data, config, roofline, cpu, settle_info, extra=None):
+    res = {
+        "metric": METRIC,
+        "value": value,
+        "unit": unit,
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dtype,
+        "data": data,
+        "config": config,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "settle": dict(settle_info, why="steps run back to back before the warm-up so that the timed steps "
+                                        "see steady GPU clocks (a power-management transient slows the first "
+                                        "few ms of a heavy load)"),
+    }
+    if extra:
+        res["extra"] = extra
+    return res
+
+
 # --------------------------------------------------------------- decode ---
 
 def bench_decode(args, dev):
+    """c3: fused decode attention at Llama-3-8B shape (headline)."""
     import smaq_amd as S
+    from smaq_amd import _native
     from smaq_amd.batch import QuantizedKVBatch
     from smaq_amd.synthetic import sample_keys, sample_values
 
@@ -70,7 +200,6 @@ def bench_decode(args, dev):
     strat = S.SMAQFullMetricScalarStrategy(D, bits=bits, device=dev).fit(calib)
     keys = sample_keys(B * N * Hkv, seed=11, device=dev, dtype=torch.bfloat16).view(B, N, Hkv, D)
     vals = sample_values(B * N * Hkv, seed=12, device=dev, dtype=torch.bfloat16).view(B, N, Hkv, D)
-    from smaq_amd import _native
     strat.quantizer.tie_counter = _native.TieCounter(dev)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -82,53 +211,44 @@ def bench_decode(args, dev):
     bytes_per_th = kvb.nbytes_per_token_head()
     algo_bytes = B * N * Hkv * bytes_per_th
     plan = kvb.plan(q)
-
-    for _ in range(args.warmup):
-        plan.run(q)
-    torch.cuda.synchronize()
     # timed region: K whole decode steps (query load + rotate, history
     # partials, split combine), no events inside
-    start, end = _events(2)
-    start.record()
-    for _ in range(args.steps):
-        plan.run(q)
-    end.record()
-    torch.cuda.synchronize()
-    ms_step = start.elapsed_time(end) / args.steps
-    # dominant kernel: HIP events on its launch stream (torch's current
-    # stream, which the plan launches on) around the history phase alone
-    kern_ms = history_kernel_ms(plan, q, args.steps)
-    achieved = algo_bytes / (kern_ms * 1e-3) / 1e9
-    traffic = recorded_traffic("decode_mfma_c3", dict(batch=B, context=N))
+    ms_step, st = time_steps(lambda: plan.run(q), args)
+    plan.load_query(q)
+    kern = kernel_ms(lambda: plan.launch(phases=1), args.steps)
+    achieved = algo_bytes / (kern * 1e-3) / 1e9
+    cpu = None if args.no_cpu_baseline else cpu_baseline_decode(strat, keys, vals, q, Hq, Hkv, D, bits)
+    del keys, vals
+    return _record(
+        args, value=B / (ms_step * 1e-3), unit="tokens/s", ms_step=ms_step, dtype=DECODE_DTYPE,
+        data="synthetic (seeded N(0, U diag(1/i) U^T) keys, N(0,1) values)",
+        config={"workload": "c3 fused decode attention, Llama-3-8B shape", "batch": B, "context": N,
+                "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "key_bits": bits, "value_bits": 2,
+                "value_group": 32, "storage_dtype": "bf16", "layout": "contiguous FlatCache"},
+        roofline={"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                  "frac": achieved / HBM_PEAK_GBS,
+                  "traffic": recorded_traffic("decode_mfma_c3", dict(batch=B, context=N)),
+                  "kernel": "decode_mfma_kernel", "kernel_ms": kern,
+                  "algorithmic_bytes": algo_bytes, "bytes_per_token_head": bytes_per_th},
+        cpu=cpu, settle_info=st,
+        extra={"encode_cache_s": encode_s, "encode_boundary_ties": ties,
+               "hbm_gbs_whole_step": algo_bytes / (ms_step * 1e-3) / 1e9})
 
-    cpu = None
-    if not args.no_cpu_baseline:
-        cpu = cpu_baseline_decode(strat, keys, vals, q, Hq, Hkv, D, bits)
-    res = {
-        "metric": METRIC,
-        "value": B / (ms_step * 1e-3),
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": ms_step,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic (seeded N(0, U diag(1/i) U^T) keys, N(0,1) values)",
-        "config": {"workload": "c3 fused decode attention, Llama-3-8B shape", "batch": B, "context": N,
-                   "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "key_bits": bits, "value_bits": 2,
-                   "value_group": 32, "storage_dtype": "bf16", "layout": "contiguous FlatCache"},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
-                     "kernel": "decode_mfma_kernel", "kernel_ms": kern_ms,
-                     "algorithmic_bytes": algo_bytes, "bytes_per_token_head": bytes_per_th},
-        "cpu_baseline": cpu,
-        "extra": {"encode_cache_s": encode_s, "encode_boundary_ties": ties,
-                  "hbm_gbs_whole_step": algo_bytes / (ms_step * 1e-3) / 1e9},
-    }
-    return res
+
+def cpu_baseline_decode(strat, keys, vals, q, Hq, Hkv, D, bits):
+    """CPU oracle decoding one sequence of the batch: all KV heads, full
+    context.  Encoding is not timed."""
+    from oracle import smaq_ref as R
+    qz = strat.quantizer
+    codec = R.ScalarCodec(D, bits, E=qz.E.cpu(), E_inv=qz.E_inv.cpu())
+    st = R.Store(codec, D, Hkv)
+    st.append_chunk(keys[0].cpu(), vals[0].cpu())
+    st.get_flat_cache()
+    qc = q[0:1].cpu()
+    t = _median_time(lambda: R.hybrid_attention(qc, st, None, None, Hq))
+    return dict({"value": 1.0 / t, "unit": "tokens/s", "kind": "port",
+                 "sample": f"1 of {keys.shape[0]} sequences (all {Hkv} KV heads, {keys.shape[1]} tokens), "
+                           f"median of 3 after 1 warm-up; {t * 1e3:.1f} ms per sequence-step"}, **_cpu_fields())
 
 
 # ---------------------------------------------------------------- paged ---
@@ -140,31 +260,17 @@ def bench_paged(args, dev):
     import smaq_amd as S
     from smaq_amd import _native
     from smaq_amd.batch import PagedQuantizedKV, _encode_rows
-    from smaq_amd.synthetic import sample_keys
+    from smaq_amd.synthetic import paged_lengths_and_table, sample_keys, student_t
 
-    g = torch.Generator().manual_seed(4)
     B, Hq, Hkv, D, bs = args.paged_seqs, 32, 8, 128, 16
-    lens = torch.randint(1024, 16385, (B,), generator=g)
-    nblk = (lens + bs - 1) // bs
-    total = int(nblk.sum())
-    perm = torch.randperm(total, generator=g)
-    table = torch.zeros(B, int(nblk.max()), dtype=torch.int32)
-    o = 0
-    for b in range(B):
-        table[b, :nblk[b]] = perm[o:o + nblk[b]].to(torch.int32)
-        o += int(nblk[b])
+    lens, table, total = paged_lengths_and_table(B, bs, seed=4)
     strat = S.SMAQFullMetricScalarStrategy(D, bits=3, device=dev).fit(sample_keys(64, seed=3))
     gd = torch.Generator(device=dev).manual_seed(41)
-    # Student-t(3) = N(0,1) / sqrt(chi2_3 / 3), drawn per element on the device
-    def student_t(shape):
-        z = torch.randn(shape, generator=gd, device=dev)
-        chi = torch.randn((*shape, 3), generator=gd, device=dev).square().sum(-1) / 3.0
-        return (z / chi.sqrt()).to(torch.bfloat16)
     kp = torch.empty(total, bs, Hkv, D, dtype=torch.bfloat16, device=dev)
     vp = torch.empty_like(kp)
     for i in range(0, total, 8192):
         j = min(total, i + 8192)
-        kp[i:j] = student_t((j - i, bs, Hkv, D))
+        kp[i:j] = student_t((j - i, bs, Hkv, D), gd, dev)
         vp[i:j] = torch.randn((j - i, bs, Hkv, D), generator=gd, device=dev).to(torch.bfloat16)
     strat.quantizer.tie_counter = _native.TieCounter(dev)
     codes, norms, vd, vsc, vz = _encode_rows(strat, kp.permute(0, 2, 1, 3), vp.permute(0, 2, 1, 3), 2, 32)
@@ -174,232 +280,24 @@ def bench_paged(args, dev):
     plan = pk.plan(q)
     token_heads = int(lens.sum()) * Hkv
     algo = token_heads * pk.nbytes_per_token_head()
-    for _ in range(args.warmup):
-        plan.run(q)
-    torch.cuda.synchronize()
-    start, end = _events(2)
-    start.record()
-    for _ in range(args.steps):
-        plan.run(q)
-    end.record()
-    torch.cuda.synchronize()
-    ms_step = start.elapsed_time(end) / args.steps
-    kern_ms = history_kernel_ms(plan, q, args.steps)
-    achieved = algo / (kern_ms * 1e-3) / 1e9
+    ms_step, st = time_steps(lambda: plan.run(q), args)
+    plan.load_query(q)
+    kern = kernel_ms(lambda: plan.launch(phases=1), args.steps)
+    achieved = algo / (kern * 1e-3) / 1e9
     cpu = None if args.no_cpu_baseline else cpu_baseline_paged(strat, table, lens, bs, codes, norms, vd, vsc, vz,
                                                                   q, Hq, Hkv, D)
-    return {
-        "metric": METRIC,
-        "value": B / (ms_step * 1e-3),
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": ms_step,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic (Student-t(3) keys, N(0,1) values, seeded lengths and block tables)",
-        "config": {"workload": "c5 paged decode", "seqs": B, "block_size": bs, "q_heads": Hq, "kv_heads": Hkv,
-                   "head_dim": D, "key_bits": 3, "value_bits": 2, "value_group": 32, "storage_dtype": "bf16",
-                   "total_tokens": int(lens.sum()), "physical_blocks": total},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": recorded_traffic("decode_mfma_paged_c5", dict(seqs=B, total_tokens=int(lens.sum()))),
-                     "kernel": "decode_mfma_kernel",
-                     "kernel_ms": kern_ms, "algorithmic_bytes": algo,
-                     "bytes_per_token_head": pk.nbytes_per_token_head()},
-        "cpu_baseline": cpu,
-        "extra": {"encode_boundary_ties": strat.quantizer.tie_counter.value()},
-    }
-
-
-# -------------------------------------------------------------- prefill ---
-
-def bench_prefill(args, dev):
-    """c4: hybrid chunked prefill at Qwen2-7B shape: 28 query / 4 KV heads,
-    2048 causal queries over 65408 block-VQ history tokens (block_dim 2, 256
-    centroids = 4 bits/dim, 4 outlier channels x20) + 128 fp16 recent tokens,
-    2-bit values."""
-    import smaq_amd as S
-    from smaq_amd import _native
-    from smaq_amd.synthetic import sample_keys, sample_values
-
-    Hq, Hkv, D = 28, 4, 128
-    N, R, T = args.prefill_context - 128, 128, args.prefill_queries
-    g = torch.Generator().manual_seed(3)
-    outl = torch.randperm(D, generator=g)[:4]
-    calib_k = sample_keys(4096, seed=31)
-    calib_k[:, outl] *= 20
-    calib_q = sample_keys(4096, seed=32)
-    strat = S.SMAQBlockVQStrategy(D, block_dim=2, n_centroids=256, device=dev)
-    strat.quantizer.fit(calib_k, calib_q, kmeans_iters=args.fit_iters)
-    keys = sample_keys(N * Hkv, seed=33, device=dev, dtype=torch.float16).view(N, Hkv, D)
-    keys[..., outl.to(dev)] *= 20
-    vals = sample_values(N * Hkv, seed=34, device=dev, dtype=torch.float16).view(N, Hkv, D)
-    st = S.CompressedKVStore(D, Hkv, device=dev, key_strategy=strat)
-    st.append_chunk(keys, vals)
-    kr = sample_keys(R * Hkv, seed=35, device=dev, dtype=torch.float16).view(R, Hkv, D)
-    kr[..., outl.to(dev)] *= 20
-    vr = sample_values(R * Hkv, seed=36, device=dev, dtype=torch.float16).view(R, Hkv, D)
-    q = sample_keys(T * Hq, seed=37, device=dev, dtype=torch.float16).view(T, Hq, D)
-    pos = torch.arange(N + R - T, N + R, device=dev)
-    from smaq_amd.score import plan_hybrid_attention
-    plan = plan_hybrid_attention(q, st, kr, vr, Hq, query_positions=pos)
-    q1 = q.unsqueeze(0)
-
-    def step():
-        return plan.run(q1)
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    start, end = _events(2)
-    start.record()
-    for _ in range(args.steps):
-        step()
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.steps
-    # history phase alone (block-VQ keys -> f16 planes, then the matrix-core
-    # kernel), events on its launch stream
-    kern_ms = history_kernel_ms(plan, q1, args.steps)
-    # QK + PV multiply-adds over the causal pairs, 2 flops each
-    pairs = sum(min(int(p) + 1, N + R) for p in pos.tolist()) * Hq
-    flops = pairs * D * 2 * 2
-    hist_pairs = sum(min(int(p) + 1, N) for p in pos.tolist()) * Hq
-    hist_flops = hist_pairs * D * 2 * 2
-    byts = N * Hkv * (64 + 32 + 8 + 8) + R * Hkv * D * 2 * 2 + T * Hq * D * 2 * 2
-    cpu = None if args.no_cpu_baseline else cpu_baseline_prefill(strat, st, kr, vr, q, pos, Hq, Hkv, D)
-    return {
-        "metric": METRIC,
-        "value": T / (ms * 1e-3),
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": ms,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic (seeded keys with 4 outlier channels x20, N(0,1) values)",
-        "config": {"workload": "c4 hybrid chunked prefill, Qwen2-7B shape", "q_heads": Hq, "kv_heads": Hkv,
-                   "head_dim": D, "queries": T, "history": N, "recent": R, "key_format": "block-VQ bd=2 nc=256",
-                   "value_bits": 2, "storage_dtype": "fp16", "causal": True},
-        "roofline": {"bound": "mfma", "achieved": hist_flops / (kern_ms * 1e-3) / 1e12, "peak": 2500.0,
-                     "unit": "TFLOP/s", "frac": hist_flops / (kern_ms * 1e-3) / 1e12 / 2500.0, "traffic": None,
-                     "kernel": "prefill_mfma_kernel (history phase, with decode_hist_planes_kernel)",
-                     "kernel_ms": kern_ms, "algorithmic_flops": hist_flops, "step_flops": flops,
-                     "step_tflops": flops / (ms * 1e-3) / 1e12, "algorithmic_bytes": byts},
-        "cpu_baseline": cpu,
-    }
-
-
-# --------------------------------------------------------------- encode ---
-
-def bench_encode(args, dev):
-    """c2: block-VQ key encode + 2-bit value pack of [16 seq x 32768 tok x 8
-    heads x 128] bf16 keys and values (4.19M token-heads), cache resident in
-    HBM.  One step = encode every key (16 uint8 indices per token-head) and
-    pack every value (32 B codes + 4 bf16 scales + 4 bf16 zeros)."""
-    import smaq_amd as S
-    from smaq_amd import _native
-    from smaq_amd.kv_cache import quantize_values
-    from smaq_amd.synthetic import sample_keys, sample_values
-
-    seqs, toks, H, D = 16, args.encode_tokens, 8, 128
-    rows = seqs * toks * H
-    strat = S.SMAQBlockVQStrategy(D, block_dim=8, n_centroids=256, device=dev)
-    calib_k = sample_keys(args.fit_samples, seed=21)
-    calib_q = sample_keys(args.fit_samples, seed=22)
-    t_fit = time.perf_counter()
-    strat.quantizer.fit(calib_k, calib_q, kmeans_iters=args.fit_iters)
-    t_fit = time.perf_counter() - t_fit
-    keys = sample_keys(rows, seed=23, device=dev, dtype=torch.bfloat16).view(seqs, toks, H, D)
-    vals = sample_values(rows, seed=24, device=dev, dtype=torch.bfloat16).view(seqs, toks, H, D)
-    strat.quantizer.tie_counter = _native.TieCounter(dev)
-
-    def step():
-        strat.quantize(keys)
-        quantize_values(vals, bits=2, group_size=32)
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    start, end = _events(2)
-    start.record()
-    for _ in range(args.steps):
-        step()
-    end.record()
-    torch.cuda.synchronize()
-    ms_step = start.elapsed_time(end) / args.steps
-    # the two kernels alone, events on the launch stream
-    ka, kb, va, vb = _events(4)
-    ka.record(); strat.quantize(keys); kb.record()
-    va.record(); quantize_values(vals, bits=2, group_size=32); vb.record()
-    torch.cuda.synchronize()
-    k_ms, v_ms = ka.elapsed_time(kb), va.elapsed_time(vb)
-    bytes_per_th = 2 * D * 2 + 16 + 32 + 16      # K + V in; indices, codes, scales/zeros out
-    algo = rows * bytes_per_th
-    flops = rows * 16 * (8 * 8 + 256 * 8) * 2
-    ties = strat.quantizer.tie_counter.value()
-    cpu = None if args.no_cpu_baseline else cpu_baseline_encode(strat, keys, vals)
-    return {
-        "metric": METRIC,
-        "value": algo / (ms_step * 1e-3) / 1e9,
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": ms_step,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic (seeded N(0, U diag(1/i) U^T) keys, N(0,1) values)",
-        "config": {"workload": "c2 block-VQ key encode + 2-bit value pack", "seqs": seqs, "tokens": toks,
-                   "kv_heads": H, "head_dim": D, "block_dim": 8, "n_centroids": 256, "storage_dtype": "bf16",
-                   "codebook_fit": f"k-means++ on {args.fit_samples} samples, {args.fit_iters} Lloyd iterations "
-                                   f"(host, {t_fit:.1f} s, untimed)"},
-        # the fp32-accurate distance contraction (8 dims x 256 centroids x 2
-        # per token-block) against the FP32 matrix peak; the kernel issues it
-        # as f16 hi/lo products (one 16x16x32 f16 MFMA per 16 centroids x 16
-        # tokens), and its limiter is VALU issue for the argmin
-        "roofline": {"bound": "mfma", "kernel": "encode_blockvq", "kernel_ms": k_ms,
-                     "achieved": rows * 16 * 256 * 8 * 2 / (k_ms * 1e-3) / 1e12,
-                     "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": rows * 16 * 256 * 8 * 2 / (k_ms * 1e-3) / 1e12 / FP32_PEAK_TFLOPS,
-                     "traffic": recorded_traffic("encode_blockvq_c2", dict(rows=rows)), "pack_values_ms": v_ms,
-                     "hbm_gbs": algo / ((k_ms + v_ms) * 1e-3) / 1e9, "algorithmic_bytes": algo,
-                     "algorithmic_flops": flops,
-                     # 16 blocks x 16 MFMAs (16 x 16 x 32 x 2 flop) per 16 tokens
-                     "issued_f16_tflops": rows * 16 * 16 * (16 * 16 * 32 * 2) / 16 / (k_ms * 1e-3) / 1e12,
-                     "f16_peak": 2500.0},
-        "cpu_baseline": cpu,
-        "extra": {"boundary_ties": ties},
-    }
-
-
-def cpu_baseline_encode(strat, keys, vals, n: int = 2048):
-    """CPU oracle encoding n token-heads (block-VQ keys + value pack)."""
-    from oracle import smaq_ref as R
-    qz = strat.quantizer
-    kc = keys.reshape(-1, keys.shape[-1])[:n].cpu()
-    vc = vals.reshape(-1, vals.shape[-1])[:n].cpu()
-    Eb, C = qz.E_blocks.cpu(), qz.centroids.cpu()
-    R.blockvq_encode(kc, Eb, C)
-    R.quantize_values(vc, bits=2, group_size=32)
-    times = []
-    for _ in range(3):
-        t = time.perf_counter()
-        R.blockvq_encode(kc, Eb, C)
-        R.quantize_values(vc, bits=2, group_size=32)
-        times.append(time.perf_counter() - t)
-    t = statistics.median(times)
-    return {"value": n * (2 * 256 + 64) / t / 1e9, "unit": "GB/s", "cores": _cores(), "kind": "port",
-            "sample": f"{n} token-heads, median of 3 after 1 warm-up ({t * 1e3:.1f} ms)"}
+    return _record(
+        args, value=B / (ms_step * 1e-3), unit="tokens/s", ms_step=ms_step, dtype=DECODE_DTYPE,
+        data="synthetic (Student-t(3) keys, N(0,1) values, seeded lengths and block tables)",
+        config={"workload": "c5 paged decode", "seqs": B, "block_size": bs, "q_heads": Hq, "kv_heads": Hkv,
+                "head_dim": D, "key_bits": 3, "value_bits": 2, "value_group": 32, "storage_dtype": "bf16",
+                "total_tokens": int(lens.sum()), "physical_blocks": total},
+        roofline={"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                  "frac": achieved / HBM_PEAK_GBS,
+                  "traffic": recorded_traffic("decode_mfma_paged_c5", dict(seqs=B, total_tokens=int(lens.sum()))),
+                  "kernel": "decode_mfma_kernel (paged)", "kernel_ms": kern, "algorithmic_bytes": algo,
+                  "bytes_per_token_head": pk.nbytes_per_token_head()},
+        cpu=cpu, settle_info=st, extra={"encode_boundary_ties": strat.quantizer.tie_counter.value()})
 
 
 class _FlatStore:
@@ -413,16 +311,6 @@ class _FlatStore:
 
     def get_flat_cache(self):
         return self.flat
-
-
-def _median_time(fn, reps: int = 3) -> float:
-    fn()  # warm-up
-    times = []
-    for _ in range(reps):
-        t = time.perf_counter()
-        fn()
-        times.append(time.perf_counter() - t)
-    return statistics.median(times)
 
 
 def cpu_baseline_paged(strat, table, lens, bs, codes, norms, vd, vsc, vz, q, Hq, Hkv, D):
@@ -447,10 +335,69 @@ def cpu_baseline_paged(strat, table, lens, bs, codes, norms, vd, vsc, vz, q, Hq,
     qc = q[b:b + 1].cpu()
     t = _median_time(lambda: R.hybrid_attention(qc, st, None, None, Hq))
     t_batch = t * float(lens.sum()) / L
-    return {"value": len(lens) / t_batch, "unit": "tokens/s", "cores": _cores(), "kind": "port",
-            "sample": f"sequence {b} ({L} tokens, the median length; all {Hkv} KV heads; codes from the GPU "
-                      f"pool), median of 3 after 1 warm-up, {t * 1e3:.1f} ms; scaled to the batch by "
-                      f"{int(lens.sum())} / {L} tokens"}
+    return dict({"value": len(lens) / t_batch, "unit": "tokens/s", "kind": "port",
+                 "sample": f"sequence {b} ({L} tokens, the median length; all {Hkv} KV heads; codes from the GPU "
+                           f"pool), median of 3 after 1 warm-up, {t * 1e3:.1f} ms; scaled to the batch by "
+                           f"{int(lens.sum())} / {L} tokens"}, **_cpu_fields())
+
+
+# -------------------------------------------------------------- prefill ---
+
+def bench_prefill(args, dev):
+    """c4: hybrid chunked prefill at Qwen2-7B shape: 28 query / 4 KV heads,
+    2048 causal queries over 65408 block-VQ history tokens (block_dim 2, 256
+    centroids = 4 bits/dim, 4 outlier channels x20) + 128 fp16 recent tokens,
+    2-bit values."""
+    import smaq_amd as S
+    from smaq_amd.score import plan_hybrid_attention
+    from smaq_amd.synthetic import sample_keys, sample_values
+
+    Hq, Hkv, D = 28, 4, 128
+    N, R, T = args.prefill_context - 128, 128, args.prefill_queries
+    g = torch.Generator().manual_seed(3)
+    outl = torch.randperm(D, generator=g)[:4]
+    calib_k = sample_keys(4096, seed=31)
+    calib_k[:, outl] *= 20
+    calib_q = sample_keys(4096, seed=32)
+    strat = S.SMAQBlockVQStrategy(D, block_dim=2, n_centroids=256, device=dev)
+    strat.quantizer.fit(calib_k, calib_q, kmeans_iters=args.fit_iters)
+    keys = sample_keys(N * Hkv, seed=33, device=dev, dtype=torch.float16).view(N, Hkv, D)
+    keys[..., outl.to(dev)] *= 20
+    vals = sample_values(N * Hkv, seed=34, device=dev, dtype=torch.float16).view(N, Hkv, D)
+    st = S.CompressedKVStore(D, Hkv, device=dev, key_strategy=strat)
+    st.append_chunk(keys, vals)
+    kr = sample_keys(R * Hkv, seed=35, device=dev, dtype=torch.float16).view(R, Hkv, D)
+    kr[..., outl.to(dev)] *= 20
+    vr = sample_values(R * Hkv, seed=36, device=dev, dtype=torch.float16).view(R, Hkv, D)
+    q = sample_keys(T * Hq, seed=37, device=dev, dtype=torch.float16).view(T, Hq, D)
+    pos = torch.arange(N + R - T, N + R, device=dev)
+    plan = plan_hybrid_attention(q, st, kr, vr, Hq, query_positions=pos)
+    q1 = q.unsqueeze(0)
+    ms, st_info = time_steps(lambda: plan.run(q1), args)
+    # history phase alone (block-VQ keys -> f16 tile images, then the
+    # matrix-core kernel), events on its launch stream
+    plan.load_query(q1)
+    kern = kernel_ms(lambda: plan.launch(phases=1), args.steps)
+    # QK + PV multiply-adds over the causal pairs, 2 flops each
+    pairs = sum(min(int(p) + 1, N + R) for p in pos.tolist()) * Hq
+    flops = pairs * D * 2 * 2
+    hist_pairs = sum(min(int(p) + 1, N) for p in pos.tolist()) * Hq
+    hist_flops = hist_pairs * D * 2 * 2
+    byts = N * Hkv * (64 + 32 + 8 + 8) + R * Hkv * D * 2 * 2 + T * Hq * D * 2 * 2
+    cpu = None if args.no_cpu_baseline else cpu_baseline_prefill(strat, st, kr, vr, q, pos, Hq, Hkv, D)
+    achieved = hist_flops / (kern * 1e-3) / 1e12
+    return _record(
+        args, value=T / (ms * 1e-3), unit="tokens/s", ms_step=ms, dtype=PREFILL_DTYPE,
+        data="synthetic (seeded keys with 4 outlier channels x20, N(0,1) values)",
+        config={"workload": "c4 hybrid chunked prefill, Qwen2-7B shape", "q_heads": Hq, "kv_heads": Hkv,
+                "head_dim": D, "queries": T, "history": N, "recent": R, "key_format": "block-VQ bd=2 nc=256",
+                "value_bits": 2, "storage_dtype": "fp16", "causal": True},
+        roofline={"bound": "mfma", "achieved": achieved, "peak": F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                  "frac": achieved / F16_PEAK_TFLOPS, "traffic": None,
+                  "kernel": "prefill_mfma_kernel (history phase, with decode_hist_planes_kernel)",
+                  "kernel_ms": kern, "algorithmic_flops": hist_flops, "step_flops": flops,
+                  "step_tflops": flops / (ms * 1e-3) / 1e12, "algorithmic_bytes": byts},
+        cpu=cpu, settle_info=st_info)
 
 
 def cpu_baseline_prefill(strat, st, kr, vr, q, pos, Hq, Hkv, D, n_q: int = 64):
@@ -467,81 +414,110 @@ def cpu_baseline_prefill(strat, st, kr, vr, q, pos, Hq, Hkv, D, n_q: int = 64):
     ost = _FlatStore(flat, codec, D, Hkv)
     qs, ps, krc, vrc = q[-n_q:].cpu(), pos[-n_q:].cpu(), kr.cpu(), vr.cpu()
     t = _median_time(lambda: R.hybrid_attention(qs, ost, krc, vrc, Hq, query_positions=ps))
-    return {"value": n_q / t, "unit": "tokens/s", "cores": _cores(), "kind": "port",
-            "sample": f"the last {n_q} of {q.shape[0]} query tokens over the full context "
-                      f"({gf.num_tokens} history + {kr.shape[0]} recent), median of 3 after 1 warm-up, "
-                      f"{t * 1e3:.1f} ms"}
+    return dict({"value": n_q / t, "unit": "tokens/s", "kind": "port",
+                 "sample": f"the last {n_q} of {q.shape[0]} query tokens over the full context "
+                           f"({gf.num_tokens} history + {kr.shape[0]} recent), median of 3 after 1 warm-up, "
+                           f"{t * 1e3:.1f} ms"}, **_cpu_fields())
 
 
-def cpu_baseline_decode(strat, keys, vals, q, Hq, Hkv, D, bits):
-    """CPU oracle (op-for-op torch restatement of the reference) decoding one
-    sequence of the batch: all KV heads, full context.  Encoding is not timed."""
+# --------------------------------------------------------------- encode ---
+
+def bench_encode(args, dev):
+    """c2: block-VQ key encode + 2-bit value pack of [16 seq x 32768 tok x 8
+    heads x 128] bf16 keys and values (4.19M token-heads), cache resident in
+    HBM.  One step = encode every key (16 uint8 indices per token-head) and
+    pack every value (32 B codes + 4 bf16 scales + 4 bf16 zeros).  The
+    codebook is fitted untimed: k-means++ and Lloyd on the device by default
+    (``--host-fit`` runs the reference's CPU fit instead, ~50 s)."""
+    import smaq_amd as S
+    from smaq_amd import _native
+    from smaq_amd.kv_cache import quantize_values
+    from smaq_amd.synthetic import sample_keys, sample_values
+
+    seqs, toks, H, D = 16, args.encode_tokens, 8, 128
+    rows = seqs * toks * H
+    strat = S.SMAQBlockVQStrategy(D, block_dim=8, n_centroids=256, device=dev)
+    calib_k = sample_keys(args.fit_samples, seed=21)
+    calib_q = sample_keys(args.fit_samples, seed=22)
+    t_fit = time.perf_counter()
+    strat.quantizer.fit(calib_k, calib_q, kmeans_iters=args.fit_iters, on_device=not args.host_fit)
+    torch.cuda.synchronize()
+    t_fit = time.perf_counter() - t_fit
+    keys = sample_keys(rows, seed=23, device=dev, dtype=torch.bfloat16).view(seqs, toks, H, D)
+    vals = sample_values(rows, seed=24, device=dev, dtype=torch.bfloat16).view(seqs, toks, H, D)
+    strat.quantizer.tie_counter = _native.TieCounter(dev)
+
+    def step():
+        strat.quantize(keys)
+        quantize_values(vals, bits=2, group_size=32)
+
+    ms_step, st = time_steps(step, args)
+    k_ms = kernel_ms(lambda: strat.quantize(keys), args.steps)
+    v_ms = kernel_ms(lambda: quantize_values(vals, bits=2, group_size=32), args.steps)
+    bytes_per_th = 2 * D * 2 + 16 + 32 + 16      # K + V in; indices, codes, scales/zeros out
+    algo = rows * bytes_per_th
+    flops = rows * 16 * (8 * 8 + 256 * 8) * 2
+    dist_flops = rows * 16 * 256 * 8 * 2
+    ties = strat.quantizer.tie_counter.value()
+    cpu = None if args.no_cpu_baseline else cpu_baseline_encode(strat, keys, vals)
+    del keys, vals
+    fit_how = "host (the reference's CPU draw)" if args.host_fit else "device"
+    return _record(
+        args, value=algo / (ms_step * 1e-3) / 1e9, unit="GB/s", ms_step=ms_step, dtype=ENCODE_DTYPE,
+        data="synthetic (seeded N(0, U diag(1/i) U^T) keys, N(0,1) values)",
+        config={"workload": "c2 block-VQ key encode + 2-bit value pack", "seqs": seqs, "tokens": toks,
+                "kv_heads": H, "head_dim": D, "block_dim": 8, "n_centroids": 256, "storage_dtype": "bf16",
+                "codebook_fit": f"k-means++ on {args.fit_samples} samples, {args.fit_iters} Lloyd iterations "
+                                f"({fit_how}, {t_fit:.1f} s, untimed)"},
+        # the fp32-accurate distance contraction (8 dims x 256 centroids x 2
+        # per token-block) against the FP32 matrix peak; the kernel issues it
+        # as f16 hi/lo products (one 16x16x32 f16 MFMA per 16 centroids x 16
+        # tokens), and its limiter is VALU issue for the argmin
+        roofline={"bound": "mfma", "kernel": "encode_blockvq_mfma_kernel", "kernel_ms": k_ms,
+                  "achieved": dist_flops / (k_ms * 1e-3) / 1e12, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                  "frac": dist_flops / (k_ms * 1e-3) / 1e12 / FP32_PEAK_TFLOPS,
+                  "traffic": recorded_traffic("encode_blockvq_c2", dict(rows=rows)), "pack_values_ms": v_ms,
+                  "hbm_gbs": algo / ((k_ms + v_ms) * 1e-3) / 1e9, "algorithmic_bytes": algo,
+                  "algorithmic_flops": flops,
+                  # 16 blocks x 16 MFMAs (16 x 16 x 32 x 2 flop) per 16 tokens
+                  "issued_f16_tflops": rows * 16 * 16 * (16 * 16 * 32 * 2) / 16 / (k_ms * 1e-3) / 1e12,
+                  "f16_peak": F16_PEAK_TFLOPS},
+        cpu=cpu, settle_info=st, extra={"boundary_ties": ties})
+
+
+def cpu_baseline_encode(strat, keys, vals, n: int = 2048):
+    """CPU oracle encoding n token-heads (block-VQ keys + value pack)."""
     from oracle import smaq_ref as R
     qz = strat.quantizer
-    codec = R.ScalarCodec(D, bits, E=qz.E.cpu(), E_inv=qz.E_inv.cpu())
-    st = R.Store(codec, D, Hkv)
-    st.append_chunk(keys[0].cpu(), vals[0].cpu())
-    st.get_flat_cache()
-    qc = q[0:1].cpu()
-    R.hybrid_attention(qc, st, None, None, Hq)          # warm-up
-    times = []
-    for _ in range(3):
-        t = time.perf_counter()
-        R.hybrid_attention(qc, st, None, None, Hq)
-        times.append(time.perf_counter() - t)
-    t = statistics.median(times)
-    return {"value": 1.0 / t, "unit": "tokens/s", "cores": _cores(), "kind": "port",
-            "sample": f"1 of {keys.shape[0]} sequences (all {Hkv} KV heads, {keys.shape[1]} tokens), "
-                      f"median of 3 after 1 warm-up; {t * 1e3:.1f} ms per sequence-step"}
+    kc = keys.reshape(-1, keys.shape[-1])[:n].cpu()
+    vc = vals.reshape(-1, vals.shape[-1])[:n].cpu()
+    Eb, C = qz.E_blocks.cpu(), qz.centroids.cpu()
+    t = _median_time(lambda: (R.blockvq_encode(kc, Eb, C), R.quantize_values(vc, bits=2, group_size=32)))
+    return dict({"value": n * (2 * 256 + 64) / t / 1e9, "unit": "GB/s", "kind": "port",
+                 "sample": f"{n} token-heads, median of 3 after 1 warm-up ({t * 1e3:.1f} ms)"}, **_cpu_fields())
 
 
-def recorded_traffic(name: str, config: dict):
-    """HBM bytes per launch of the dominant kernel, as measured by the
-    rocprofv3 FETCH_SIZE / WRITE_SIZE passes recorded in profiles/<name>.md
-    (line ``traffic_bytes_per_launch = N``, with the config it was taken on).
-    None when no record matches this configuration."""
-    path = os.path.join(ROOT, "profiles", name + ".md")
-    if not os.path.exists(path):
-        return None
-    rec = {}
-    with open(path) as f:
-        for line in f:
-            if "=" in line and line.strip().startswith(("traffic_bytes_per_launch", *config)):
-                k, v = line.split("=", 1)
-                rec[k.strip()] = int(v.strip())
-    if "traffic_bytes_per_launch" not in rec or any(rec.get(k) != v for k, v in config.items()):
-        return None
-    return rec["traffic_bytes_per_launch"]
-
+# ---------------------------------------------------------- HBM ceiling ---
 
 def copy_ceiling(dev, nbytes: int = 1 << 30, reps: int = 10):
-    """Device-to-device copy of nbytes: the practical HBM ceiling (read +
-    write bytes / time) and the reference kernel for counter calibration."""
+    """Device-to-device copy of nbytes (read + write bytes / time) and a
+    full fp32 reduction over the same bytes (read only): the practical HBM
+    ceilings next to the 8 TB/s peak, and the reference kernel for counter
+    calibration."""
     src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
     dst = torch.empty_like(src)
-    for _ in range(2):
-        dst.copy_(src)
-    torch.cuda.synchronize()
-    a, b = _events(2)
-    a.record()
-    for _ in range(reps):
-        dst.copy_(src)
-    b.record()
-    torch.cuda.synchronize()
-    ms = a.elapsed_time(b) / reps
-    # read-only ceiling: a full reduction over the same bytes as fp32
+    ms = kernel_ms(lambda: dst.copy_(src), reps)
     xf = src.view(torch.float32)
-    for _ in range(2):
-        xf.sum()
-    torch.cuda.synchronize()
-    a.record()
-    for _ in range(reps):
-        xf.sum()
-    b.record()
-    torch.cuda.synchronize()
-    rms = a.elapsed_time(b) / reps
+    rms = kernel_ms(lambda: xf.sum(), reps)
+    del src, dst
     return {"copy_bytes": nbytes, "copy_ms": ms, "copy_gbs": 2 * nbytes / (ms * 1e-3) / 1e9,
             "read_ms": rms, "read_gbs": nbytes / (rms * 1e-3) / 1e9}
+
+
+def _summary(rec: dict) -> dict:
+    """A workload's record without the fields the headline line already has."""
+    keep = ("value", "unit", "ms_per_step", "dtype", "data", "config", "roofline", "cpu_baseline", "settle", "extra")
+    return {k: rec[k] for k in keep if k in rec}
 
 
 # --------------------------------------------------------------- main ---
@@ -549,15 +525,18 @@ def copy_ceiling(dev, nbytes: int = 1 << 30, reps: int = 10):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--workload", default="decode", choices=["decode", "encode", "paged", "prefill"])
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--settle-ms", type=float, default=300.0,
+                    help="back-to-back steps before the warm-up (ms of wall time; 0 = none)")
+    ap.add_argument("--workload", default="all", choices=["all", "decode", "encode", "paged", "prefill"])
     ap.add_argument("--prefill-context", type=int, default=65536, help="c4 context (history + 128 recent)")
     ap.add_argument("--prefill-queries", type=int, default=2048, help="c4 causal query tokens")
     ap.add_argument("--paged-seqs", type=int, default=256, help="c5 sequences")
     ap.add_argument("--encode-tokens", type=int, default=32768, help="c2 tokens per sequence")
     ap.add_argument("--fit-samples", type=int, default=65536, help="c2 codebook calibration samples")
     ap.add_argument("--fit-iters", type=int, default=20, help="c2/c4 Lloyd iterations")
+    ap.add_argument("--host-fit", action="store_true", help="c2: fit the codebook on the host CPU")
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--context", type=int, default=32768)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -573,11 +552,26 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
+    torch.set_num_threads(cpu_threads())
     dev = torch.device("cuda:0")
     if args.copy_probe:
         print(json.dumps(copy_ceiling(dev)), flush=True)
         return
-    res = {"encode": bench_encode, "paged": bench_paged, "prefill": bench_prefill}.get(args.workload, bench_decode)(args, dev)
+    one = {"decode": bench_decode, "encode": bench_encode, "paged": bench_paged, "prefill": bench_prefill}
+    if args.workload != "all":
+        print(json.dumps(one[args.workload](args, dev)), flush=True)
+        return
+    res = bench_decode(args, dev)
+    print(f"# c3 decode: {res['value']:.0f} tokens/s, kernel {res['roofline']['kernel_ms'] * 1e3:.1f} us",
+          file=sys.stderr, flush=True)
+    torch.cuda.empty_cache()
+    extra = res.setdefault("extra", {})
+    for name, fn in (("c5_paged_decode", bench_paged), ("c4_prefill", bench_prefill), ("c2_encode", bench_encode)):
+        rec = fn(args, dev)
+        extra[name] = _summary(rec)
+        print(f"# {name}: {rec['value']:.4g} {rec['unit']}", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
+    extra["hbm_ceiling"] = copy_ceiling(dev)
     print(json.dumps(res), flush=True)
 
 

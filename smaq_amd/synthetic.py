@@ -39,3 +39,29 @@ def sample_keys(n: int, d: int = 128, seed: int = 1, sigma_seed: int = 0, device
 def sample_values(n: int, d: int = 128, seed: int = 2, device="cpu", dtype=torch.float32) -> torch.Tensor:
     g = torch.Generator(device=torch.device(device)).manual_seed(seed)
     return torch.randn(n, d, generator=g, device=device).to(dtype)
+
+
+def student_t(shape, generator: torch.Generator, device, df: int = 3, dtype=torch.bfloat16) -> torch.Tensor:
+    """Heavy-tailed keys: each element Student-t(df) = N(0,1) / sqrt(chi2_df / df),
+    with the chi-square drawn as a sum of df squared normals (all from
+    `generator`, on `device`)."""
+    z = torch.randn(shape, generator=generator, device=device)
+    chi = torch.randn((*shape, df), generator=generator, device=device).square().sum(-1) / float(df)
+    return (z / chi.sqrt()).to(dtype)
+
+
+def paged_lengths_and_table(batch: int, block_size: int, seed: int, lo: int = 1024, hi: int = 16384):
+    """Sequence lengths U[lo, hi] and a shuffled block table over exactly the
+    blocks they need: (lens int64 [batch], table int32 [batch, max_blocks],
+    physical block count)."""
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(lo, hi + 1, (batch,), generator=g)
+    nblk = (lens + block_size - 1) // block_size
+    total = int(nblk.sum())
+    perm = torch.randperm(total, generator=g)
+    table = torch.zeros(batch, int(nblk.max()), dtype=torch.int32)
+    o = 0
+    for b in range(batch):
+        table[b, :nblk[b]] = perm[o:o + nblk[b]].to(torch.int32)
+        o += int(nblk[b])
+    return lens, table, total

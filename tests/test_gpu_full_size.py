@@ -11,10 +11,12 @@ workloads in seconds):
 
 c3: 32 sequences x 32768 tokens x 8 KV heads (3-bit scalar keys, bf16).
 c2: 16 x 32768 x 8 token-heads, block-VQ (8-dim blocks, 256 centroids).
-c5: 256 paged sequences, lengths U[1024, 16384], 16-token blocks.
+c5: 256 paged sequences, lengths U[1024, 16384], 16-token blocks,
+    Student-t(3) keys.
+c2: codebook fitted on 65536 samples with 20 Lloyd iterations.
 c4: 2048 causal queries (28 heads) over 65408 block-VQ history tokens
-    (block_dim 2) + 128 fp16 recent tokens; sampled query tokens against the
-    oracle run on those queries alone.
+    (block_dim 2) + 128 fp16 recent tokens; 8 query tokens from each of the
+    8 256-token query blocks against the oracle run on those queries alone.
 """
 
 from __future__ import annotations
@@ -26,6 +28,7 @@ import smaq_amd as S
 from smaq_amd import _native
 from smaq_amd.batch import PagedQuantizedKV, QuantizedKVBatch, _encode_rows
 from smaq_amd.synthetic import sample_keys as dev_sample_keys
+from smaq_amd.synthetic import paged_lengths_and_table, student_t
 from smaq_amd.synthetic import sample_values as dev_sample_values
 from oracle import smaq_ref as R
 from tests.conftest import sample_keys
@@ -85,11 +88,12 @@ def test_c3_full_size_decode(dev):
 def test_c2_full_size_encode(dev):
     seqs, toks, Hkv, D = 16, 32768, 8, 128
     rows = seqs * toks * Hkv
-    ck, cq = sample_keys(8192, seed=21), sample_keys(8192, seed=22)
-    Eb, Eib, C, Dc = R.blockvq_fit(ck, cq, block_dim=8, n_centroids=256, iters=3, seed=42)
+    # the bench's codebook: k-means++ on 65536 seeded samples, 20 Lloyd
+    # iterations (device fit; the encoder is checked against the oracle for
+    # whatever codebook it is given)
     vq = S.SMAQBlockVQ(D, block_dim=8, device=dev)
-    vq.E_blocks, vq.E_inv_blocks = Eb.to(dev), Eib.to(dev)
-    vq.centroids, vq.decoded_centroids = C.to(dev), Dc.to(dev)
+    vq.fit(sample_keys(65536, seed=21), sample_keys(65536, seed=22), kmeans_iters=20, on_device=True)
+    Eb, C = vq.E_blocks.cpu(), vq.centroids.cpu()
     keys = dev_sample_keys(rows, seed=23, device=dev, dtype=torch.bfloat16).view(seqs, toks, Hkv, D)
     vals = dev_sample_values(rows, seed=24, device=dev, dtype=torch.bfloat16).view(seqs, toks, Hkv, D)
     vq.tie_counter = _native.TieCounter(dev)
@@ -111,21 +115,17 @@ def test_c2_full_size_encode(dev):
 
 def test_c5_full_size_paged(dev):
     B, Hq, Hkv, D, bs = 256, 32, 8, 128, 16
-    g = torch.Generator().manual_seed(4)
-    lens = torch.randint(1024, 16385, (B,), generator=g)
-    nblk = (lens + bs - 1) // bs
-    total = int(nblk.sum())
-    perm = torch.randperm(total, generator=g)
-    table = torch.zeros(B, int(nblk.max()), dtype=torch.int32)
-    o = 0
-    for b in range(B):
-        table[b, :nblk[b]] = perm[o:o + nblk[b]].to(torch.int32)
-        o += int(nblk[b])
+    lens, table, total = paged_lengths_and_table(B, bs, seed=4)
     calib = sample_keys(64, seed=3)
     strat = S.SMAQFullMetricScalarStrategy(D, bits=3, device=dev).fit(calib)
+    # BASELINE c5: Student-t(3) keys per channel (the bench's draw)
     gd = torch.Generator(device=dev).manual_seed(41)
-    kp = torch.randn(total, bs, Hkv, D, generator=gd, device=dev).bfloat16()
-    vp = torch.randn(total, bs, Hkv, D, generator=gd, device=dev).bfloat16()
+    kp = torch.empty(total, bs, Hkv, D, dtype=torch.bfloat16, device=dev)
+    vp = torch.empty_like(kp)
+    for i in range(0, total, 8192):
+        j = min(total, i + 8192)
+        kp[i:j] = student_t((j - i, bs, Hkv, D), gd, dev)
+        vp[i:j] = torch.randn((j - i, bs, Hkv, D), generator=gd, device=dev).to(torch.bfloat16)
     codes, norms, vd, vsc, vz = _encode_rows(strat, kp.permute(0, 2, 1, 3), vp.permute(0, 2, 1, 3), 2, 32)
     del kp, vp
     pk = PagedQuantizedKV(strat, codes, norms, vd, vsc, vz, table.to(dev), lens.tolist(), bs, 2, 32)
@@ -176,6 +176,9 @@ def test_c4_full_size_prefill(dev):
                        R.ValueQ(gf.value_q.data.cpu(), gf.value_q.scales.cpu(), gf.value_q.zeros.cpu(),
                                 gf.value_q.bits), gf.num_tokens)
     ost = _FlatStore(flat, codec, D, Hkv)
-    for sl in (slice(0, 16), slice(T - 16, T)):
-        ref_o = R.hybrid_attention(q[sl].cpu(), ost, kr.cpu(), vr.cpu(), Hq, query_positions=pos[sl].cpu())
-        assert_attn_close(out[sl], ref_o, f"c4 full size, queries {sl.start}..{sl.stop - 1}")
+    # eight query tokens from each 256-token query block (the kernel's
+    # workgroup rows), first and last of every block included; each token's
+    # output merges every key split of the history
+    sel = torch.tensor([blk * 256 + o for blk in range(T // 256) for o in (0, 37, 74, 111, 148, 185, 222, 255)])
+    ref_o = R.hybrid_attention(q[sel.to(dev)].cpu(), ost, kr.cpu(), vr.cpu(), Hq, query_positions=pos[sel.to(dev)].cpu())
+    assert_attn_close(out[sel], ref_o, f"c4 full size, {sel.numel()} queries over {T // 256} query blocks")

@@ -1,9 +1,9 @@
 """GPU parity of the matrix-core chunked-prefill kernel (impl=3).
 
 At sizes the oracle finishes in seconds the kernel is checked against the
-CPU oracle; at larger, batched and paged shapes against the generic GPU
-kernels (impl=1), which are themselves oracle-checked in
-test_gpu_attention.py.  Tolerance as there: 2e-3 absolute + 1e-3 relative
+CPU oracle (the paged layout included, its history gathered through the
+block table); at larger and batched shapes against the generic GPU kernels
+(impl=1), which are themselves oracle-checked in test_gpu_attention.py.  Tolerance as there: 2e-3 absolute + 1e-3 relative
 (+ one output ulp for bf16/fp16 outputs).  Shapes exercise partial 64-key
 tiles, partial 128-query blocks, GQA groups, causal masks that cut tiles, and
 the history/recent split of one softmax."""
@@ -161,3 +161,29 @@ def test_prefill_paged_vs_generic(dev):
     got = pk.attention(q, impl=3, query_positions=pos)
     ref = pk.attention(q, impl=1, query_positions=pos)
     assert_attn_close(got, ref.cpu(), "prefill paged")
+    # and against the oracle: each sequence's history gathered from the GPU
+    # pool through its block table, scored by the oracle's hybrid attention
+    qz = strat.quantizer
+    codec = R.ScalarCodec(128, 4, E=qz.E.cpu(), E_inv=qz.E_inv.cpu())
+    for b, n in enumerate(lens):
+        blocks = table[b, :nblk[b]].long().to(dev)
+
+        def gather(x):  # pool [blocks, Hkv, bs, ...] -> [Hkv, n, ...]
+            return x[blocks].transpose(0, 1).reshape(2, nblk[b] * bs, *x.shape[3:])[:, :n].cpu().contiguous()
+
+        flat = R.FlatCache(R.ScalarQ(gather(pk.codes), gather(pk.norms), 4),
+                           R.ValueQ(gather(pk.v_data), gather(pk.v_scales), gather(pk.v_zeros), 2), n)
+        ost = _OracleFlatStore(flat, codec, 128, 2)
+        ref_o = R.hybrid_attention(q[b].cpu(), ost, None, None, 8, query_positions=pos[b].cpu())
+        assert_attn_close(got[b], ref_o, f"prefill paged vs oracle, sequence {b} ({n} tokens)")
+
+
+class _OracleFlatStore:
+    """The oracle store interface over a flat cache built from GPU codes."""
+
+    def __init__(self, flat, codec, head_dim, num_kv_heads):
+        self.flat, self.codec = flat, codec
+        self.head_dim, self.num_kv_heads, self.value_group_size = head_dim, num_kv_heads, 32
+
+    def get_flat_cache(self):
+        return self.flat

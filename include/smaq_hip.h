@@ -13,9 +13,13 @@
  *    smaq_attn_hybrid_noalloc, whose workspace is one built-in array per GPU.
  *  - dtype codes: SMAQ_F32 = 0, SMAQ_F16 = 1, SMAQ_BF16 = 2.
  *  - "rows" inputs are addressed as row r = o * n_inner + i at element offset
- *    o * s_outer + i * s_inner with a contiguous last dim; outputs are dense
- *    row-major in r order.  This covers the [1, Hkv, T, D] transpose views the
- *    reference's store passes to its codecs (smaq/store.py:86-87).
+ *    o * s_outer + i * s_inner with a contiguous last dim.  This covers the
+ *    [1, Hkv, T, D] transpose views the reference's store passes to its codecs
+ *    (smaq/store.py:86-87).  The encoders write row r to output row
+ *    o * out_outer + i: out_outer = 0 means n_inner (dense, row-major in r
+ *    order); a larger out_outer writes into the tail rows of per-head columns
+ *    [Hkv][capacity][...] (pass the column base offset by the first new row
+ *    and out_outer = capacity), so an appended chunk is encoded in place.
  *
  * Each declaration names the reference interface (file:line under
  * gauravsaini/smaq) whose arithmetic it replaces.
@@ -44,8 +48,8 @@ const char* smaq_last_error(void);
  *   data_out   [rows, D/vpb] uint8     scales_out, zeros_out [rows, D/group] vdtype
  */
 int smaq_pack_values(const void* v, int vdtype, long long n_outer, long long n_inner,
-                     long long s_outer, long long s_inner, int D, int bits, int group,
-                     void* data_out, void* scales_out, void* zeros_out, void* stream);
+                     long long s_outer, long long s_inner, long long out_outer, int D, int bits,
+                     int group, void* data_out, void* scales_out, void* zeros_out, void* stream);
 
 /*
  * Value dequantiser.  Replaces unpack_values + dequantize_values
@@ -64,7 +68,7 @@ int smaq_dequant_values(const void* data, const void* scales, const void* zeros,
  *   tie_count (nullable): += number of y within 1e-6 (relative) of a bound.
  */
 int smaq_encode_scalar(const void* k, int kdtype, long long n_outer, long long n_inner,
-                       long long s_outer, long long s_inner, int D, const float* Mt,
+                       long long s_outer, long long s_inner, long long out_outer, int D, const float* Mt,
                        const float* coord_scales, const float* bounds, int n_bounds, int bits,
                        void* codes_out, void* norms_out, unsigned long long* tie_count,
                        void* stream);
@@ -109,7 +113,7 @@ int smaq_scores_scalar(const float* qrot, long long batch, long long nq, long lo
  *   are within 1e-6 (relative).
  */
 int smaq_encode_blockvq(const void* k, int kdtype, long long n_outer, long long n_inner,
-                        long long s_outer, long long s_inner, int n_blocks, int block_dim,
+                        long long s_outer, long long s_inner, long long out_outer, int n_blocks, int block_dim,
                         int n_centroids, const float* E_blocks, const float* centroids,
                         void* idx_out, unsigned long long* tie_count, void* stream);
 

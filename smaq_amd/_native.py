@@ -58,11 +58,11 @@ class AttnParams(ctypes.Structure):
 _SIGS = {
     "smaq_version": (c_int, []),
     "smaq_last_error": (ctypes.c_char_p, []),
-    "smaq_pack_values": (c_int, [c_void_p, c_int, c_ll, c_ll, c_ll, c_ll, c_int, c_int, c_int,
+    "smaq_pack_values": (c_int, [c_void_p, c_int, c_ll, c_ll, c_ll, c_ll, c_ll, c_int, c_int, c_int,
                                  c_void_p, c_void_p, c_void_p, c_void_p]),
     "smaq_dequant_values": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_ll, c_int, c_int,
                                     c_int, c_void_p, c_void_p]),
-    "smaq_encode_scalar": (c_int, [c_void_p, c_int, c_ll, c_ll, c_ll, c_ll, c_int, c_void_p,
+    "smaq_encode_scalar": (c_int, [c_void_p, c_int, c_ll, c_ll, c_ll, c_ll, c_ll, c_int, c_void_p,
                                    c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p,
                                    c_void_p, c_void_p]),
     "smaq_rotate_rows": (c_int, [c_void_p, c_int, c_ll, c_int, c_void_p, c_void_p, c_void_p,
@@ -71,7 +71,7 @@ _SIGS = {
                                     c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
     "smaq_scores_scalar": (c_int, [c_void_p, c_ll, c_ll, c_ll, c_int, c_void_p, c_int, c_void_p,
                                    c_int, c_void_p, c_int, c_float, c_void_p, c_int, c_void_p]),
-    "smaq_encode_blockvq": (c_int, [c_void_p, c_int, c_ll, c_ll, c_ll, c_ll, c_int, c_int, c_int,
+    "smaq_encode_blockvq": (c_int, [c_void_p, c_int, c_ll, c_ll, c_ll, c_ll, c_ll, c_int, c_int, c_int,
                                     c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "smaq_dequant_blockvq": (c_int, [c_void_p, c_ll, c_int, c_int, c_int, c_void_p, c_void_p,
                                      c_void_p]),
@@ -186,15 +186,51 @@ def _rows_args(x: torch.Tensor):
     return x, rv
 
 
+def _column_rows(x: torch.Tensor, outs):
+    """Row mapping for an encode whose outputs are views into per-head
+    columns: x is [O, I, D] (last dim contiguous), every output is [O, I,
+    *tail] with a dense tail, consecutive rows along I and O-rows a common
+    multiple apart (a [Hkv, capacity, ...] column sliced to its tail rows).
+    Returns (x, (O, I, s_outer, s_inner), out_outer) with out_outer the
+    output rows between consecutive O (0 when O == 1: dense)."""
+    if x.dim() != 3:
+        raise ValueError(f"encode into columns takes [O, I, D] input, got {tuple(x.shape)}")
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    O, I = x.shape[0], x.shape[1]
+    out_outer = None
+    for t in outs:
+        if t is None:
+            continue
+        if tuple(t.shape[:2]) != (O, I):
+            raise ValueError(f"output view {tuple(t.shape)} does not match the input rows [{O}, {I}]")
+        row = 1
+        for s in t.shape[2:]:
+            row *= s
+        tail_ok = t.dim() == 2 or t[0, 0].is_contiguous()
+        if not tail_ok or (I > 1 and t.stride(1) != row) or (O > 1 and t.stride(0) % row):
+            raise ValueError("output view rows must be dense along the token dim")
+        oo = t.stride(0) // row if O > 1 else 0
+        if out_outer is None:
+            out_outer = oo
+        elif oo != out_outer:
+            raise ValueError("output views disagree on their head stride")
+    if out_outer is not None and O > 1 and out_outer < I:
+        raise ValueError("output views overlap (head stride below the token count)")
+    return x, (O, I, x.stride(0), x.stride(1)), (out_outer or 0)
+
+
 # ---------------------------------------------------------------- values ---
 
 def _value_row_bytes(D: int, bits: int) -> int:
     return D // (4 if bits == 2 else (2 if bits == 4 else 1))
 
 
-def pack_values(v: torch.Tensor, bits: int, group_size: int):
-    """quantize_values on the GPU -> (data u8 [..., D/vpb], scales, zeros [..., D/G])."""
-    dev = require_gpu(v)
+def pack_values(v: torch.Tensor, bits: int, group_size: int, out=None):
+    """quantize_values on the GPU -> (data u8 [..., D/vpb], scales, zeros [..., D/G]).
+    With ``out`` = (data, scales, zeros) column views (see ``_column_rows``)
+    the packed rows are written there instead and ``out`` is returned."""
+    dev = require_gpu(v, *(out or ()))
     D = v.shape[-1]
     if D % group_size != 0:
         raise ValueError(f"head_dim {D} must be divisible by group_size {group_size}")
@@ -202,11 +238,19 @@ def pack_values(v: torch.Tensor, bits: int, group_size: int):
     vpb = 4 if bits == 2 else (2 if bits == 4 else 1)
     if D % vpb != 0:
         raise ValueError(f"head_dim {D} must be divisible by {vpb} for {bits}-bit packing")
-    v, (no, ni, so, si) = _rows_args(v)
-    data = torch.empty(*lead, D // vpb, dtype=torch.uint8, device=dev)
-    scales = torch.empty(*lead, D // group_size, dtype=v.dtype, device=dev)
-    zeros = torch.empty_like(scales)
-    _check(lib().smaq_pack_values(_ptr(v), dtype_code(v.dtype), no, ni, so, si, D, bits, group_size,
+    if out is None:
+        v, (no, ni, so, si) = _rows_args(v)
+        oo = 0
+        data = torch.empty(*lead, D // vpb, dtype=torch.uint8, device=dev)
+        scales = torch.empty(*lead, D // group_size, dtype=v.dtype, device=dev)
+        zeros = torch.empty_like(scales)
+    else:
+        data, scales, zeros = out
+        if (data.dtype != torch.uint8 or scales.dtype != v.dtype or zeros.dtype != v.dtype
+                or data.shape[-1] != D // vpb or scales.shape[-1] != D // group_size or zeros.shape != scales.shape):
+            raise ValueError("pack_values: output views of the wrong dtype or width")
+        v, (no, ni, so, si), oo = _column_rows(v, out)
+    _check(lib().smaq_pack_values(_ptr(v), dtype_code(v.dtype), no, ni, so, si, oo, D, bits, group_size,
                                   _ptr(data), _ptr(scales), _ptr(zeros), _stream(dev)),
            "smaq_pack_values")
     return data, scales, zeros
@@ -241,19 +285,28 @@ class TieCounter:
 
 
 def encode_scalar(k: torch.Tensor, Mt: torch.Tensor, bounds: torch.Tensor, bits: int,
-                  coord_scales: torch.Tensor | None = None, ties: TieCounter | None = None):
-    """Scalar key encoder -> (packed codes u8 [..., ceil(D/vpb)], norms [...] in k.dtype)."""
-    dev = require_gpu(k, Mt, bounds, coord_scales)
+                  coord_scales: torch.Tensor | None = None, ties: TieCounter | None = None, out=None):
+    """Scalar key encoder -> (packed codes u8 [..., ceil(D/vpb)], norms [...] in k.dtype).
+    With ``out`` = (codes, norms) column views (see ``_column_rows``) the rows
+    are written there instead and ``out`` is returned."""
+    dev = require_gpu(k, Mt, bounds, coord_scales, *(out or ()))
     D = k.shape[-1]
     lead = k.shape[:-1]
     vpb = max(1, 8 // bits)
-    k, (no, ni, so, si) = _rows_args(k)
-    codes = torch.empty(*lead, (D + vpb - 1) // vpb, dtype=torch.uint8, device=dev)
-    norms = torch.empty(lead, dtype=k.dtype, device=dev)
+    if out is None:
+        k, (no, ni, so, si) = _rows_args(k)
+        oo = 0
+        codes = torch.empty(*lead, (D + vpb - 1) // vpb, dtype=torch.uint8, device=dev)
+        norms = torch.empty(lead, dtype=k.dtype, device=dev)
+    else:
+        codes, norms = out
+        if codes.dtype != torch.uint8 or codes.shape[-1] != (D + vpb - 1) // vpb or norms.dtype != k.dtype:
+            raise ValueError("encode_scalar: output views of the wrong dtype or width")
+        k, (no, ni, so, si), oo = _column_rows(k, out)
     Mt = Mt.to(torch.float32).contiguous()
     bounds = bounds.to(torch.float32).contiguous()
     cs = None if coord_scales is None else coord_scales.to(torch.float32).contiguous()
-    _check(lib().smaq_encode_scalar(_ptr(k), dtype_code(k.dtype), no, ni, so, si, D, _ptr(Mt), _ptr(cs),
+    _check(lib().smaq_encode_scalar(_ptr(k), dtype_code(k.dtype), no, ni, so, si, oo, D, _ptr(Mt), _ptr(cs),
                                     _ptr(bounds), bounds.numel(), bits, _ptr(codes), _ptr(norms),
                                     ties.ptr() if ties else None, _stream(dev)),
            "smaq_encode_scalar")
@@ -315,17 +368,27 @@ def scores_scalar(qrot: torch.Tensor, codes: torch.Tensor, norms: torch.Tensor, 
 # -------------------------------------------------------------- block VQ ---
 
 def encode_blockvq(k: torch.Tensor, E_blocks: torch.Tensor, centroids: torch.Tensor,
-                   ties: TieCounter | None = None) -> torch.Tensor:
-    dev = require_gpu(k, E_blocks, centroids)
+                   ties: TieCounter | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Block-VQ key encoder -> uint8 indices [..., n_blocks].  With ``out``
+    an index column view (see ``_column_rows``) the rows are written there
+    instead and ``out`` is returned."""
+    dev = require_gpu(k, E_blocks, centroids, out)
     nb, nc, bd = centroids.shape
     if k.shape[-1] != nb * bd:
         raise ValueError(f"key dim {k.shape[-1]} != n_blocks * block_dim = {nb * bd}")
     lead = k.shape[:-1]
-    k, (no, ni, so, si) = _rows_args(k)
+    if out is None:
+        k, (no, ni, so, si) = _rows_args(k)
+        oo = 0
+        idx = torch.empty(*lead, nb, dtype=torch.uint8, device=dev)
+    else:
+        if out.dtype != torch.uint8 or out.shape[-1] != nb:
+            raise ValueError("encode_blockvq: output view of the wrong dtype or width")
+        k, (no, ni, so, si), oo = _column_rows(k, (out,))
+        idx = out
     eb = E_blocks.to(torch.float32).contiguous()
     cents = centroids.to(torch.float32).contiguous()
-    idx = torch.empty(*lead, nb, dtype=torch.uint8, device=dev)
-    _check(lib().smaq_encode_blockvq(_ptr(k), dtype_code(k.dtype), no, ni, so, si, nb, bd, nc, _ptr(eb),
+    _check(lib().smaq_encode_blockvq(_ptr(k), dtype_code(k.dtype), no, ni, so, si, oo, nb, bd, nc, _ptr(eb),
                                      _ptr(cents), _ptr(idx), ties.ptr() if ties else None, _stream(dev)),
            "smaq_encode_blockvq")
     return idx

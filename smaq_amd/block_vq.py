@@ -181,6 +181,11 @@ class SMAQBlockVQ(nn.Module):
         idx = _native.encode_blockvq(k, self.E_blocks, self.centroids, ties=self.tie_counter)
         return BlockVQQuantized(indices=idx, n_blocks=self.n_blocks, block_dim=self.block_dim)
 
+    def encode_into(self, k: torch.Tensor, idx: torch.Tensor) -> None:
+        """``quantize`` of k [lanes, T, head_dim] written into the index
+        column view idx [lanes, T, n_blocks] (append-only storage)."""
+        _native.encode_blockvq(k, self.E_blocks, self.centroids, ties=self.tie_counter, out=idx)
+
     def dequantize(self, q: BlockVQQuantized) -> torch.Tensor:
         """Pre-decoded centroid lookup (smaq/block_vq.py:246-267)."""
         return _native.dequant_blockvq(q.indices, self.decoded_centroids)

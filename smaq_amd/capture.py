@@ -1,82 +1,116 @@
 """Recent-window capture (drop-in for smaq/capture.py).
 
-``RingBuffer`` keeps the newest tokens exact; once it is full, the next write
-returns the whole ring as overflow, which ``KVCaptureEngine`` hands to the
-compressed store (where the HIP encoders run).  Plain tensor copies.
+``RingBuffer`` holds the newest tokens of one layer exact, ``[capacity, Hkv,
+D]``.  Its wrap rule is the reference's (smaq/capture.py:60-91): when a write
+finds the ring full and tokens remain, the ring's whole content leaves as
+overflow and filling restarts at slot 0.  Seen as one token stream -- the
+ring's p tokens followed by the n written -- that rule cuts the stream into
+``capacity``-token windows and spills every window but the last, so a write
+is computed in one step: m = (p + n - 1) // capacity windows spill (none
+when p + n <= capacity), i.e. the ring's p tokens and the first
+m * capacity - p written tokens, and the ring keeps the remaining ones.
+
+``KVCaptureEngine`` routes tokens: prefill tails and decode tokens into the
+ring, prefill heads and ring spills into the compressed store.  A spill is
+handed to the store as two pieces -- a view of the ring's slots and a view of
+the written tokens -- which the store's HIP encoders read in place and write
+straight into its append-only columns; nothing is joined or cloned.  (The
+reference clones the ring, concatenates the pieces and re-concatenates the
+store's whole history on the next read.)
 """
 
 from __future__ import annotations
 
-from typing import Optional, TYPE_CHECKING
+from typing import Callable, Optional, Sequence, TYPE_CHECKING
 
 import torch
 
 if TYPE_CHECKING:
     from smaq_amd.store import CompressedKVStore
 
+Pieces = Sequence[tuple[torch.Tensor, torch.Tensor]]
+
 
 class RingBuffer:
-    """Fixed-capacity window of exact K/V [capacity, Hkv, D] (smaq/capture.py:18-110)."""
-
-    __slots__ = ("capacity", "num_kv_heads", "head_dim", "device", "dtype", "_k", "_v", "_pos",
-                 "_total_written")
+    """Fixed-capacity exact window of K/V [capacity, Hkv, D] (smaq/capture.py:18-110)."""
 
     def __init__(self, capacity: int, num_kv_heads: int, head_dim: int, device: torch.device,
                  dtype: torch.dtype = torch.bfloat16):
+        if capacity <= 0:
+            raise ValueError(f"ring capacity must be positive, got {capacity}")
         self.capacity = capacity
         self.num_kv_heads = num_kv_heads
         self.head_dim = head_dim
         self.device = device
         self.dtype = dtype
-        self._k = torch.zeros(capacity, num_kv_heads, head_dim, device=device, dtype=dtype)
-        self._v = torch.zeros(capacity, num_kv_heads, head_dim, device=device, dtype=dtype)
-        self._pos = 0
-        self._total_written = 0
+        self._slots_k = torch.zeros(capacity, num_kv_heads, head_dim, device=device, dtype=dtype)
+        self._slots_v = torch.zeros(capacity, num_kv_heads, head_dim, device=device, dtype=dtype)
+        self._fill = 0       # occupied slots [0, _fill)
+        self._written = 0    # tokens ever written
 
     @property
     def size(self) -> int:
-        return self._pos
+        return self._fill
 
     @property
     def total_written(self) -> int:
-        return self._total_written
+        return self._written
+
+    def _advance(self, key: torch.Tensor, value: torch.Tensor, n: int,
+                 spill: Optional[Callable[[Pieces], None]]) -> None:
+        """Write n tokens; the spilled window(s), if any, go to ``spill`` as
+        pieces in token order before any slot is overwritten (None drops
+        them).  Written tokens take the ring's dtype and device first, as
+        writing them into the slots does."""
+        if n <= 0:
+            return
+        key = key[:n].to(device=self.device, dtype=self.dtype)
+        value = value[:n].to(device=self.device, dtype=self.dtype)
+        p, C = self._fill, self.capacity
+        stream = p + n
+        spilled = (stream - 1) // C * C          # tokens of the stream that leave
+        if spilled and spill is not None:
+            pieces = []
+            if p:
+                pieces.append((self._slots_k[:p], self._slots_v[:p]))
+            pieces.append((key[:spilled - p], value[:spilled - p]))
+            spill(pieces)
+        keep_from = max(spilled - p, 0)           # first written token that stays
+        at = p if spilled == 0 else 0
+        self._slots_k[at:at + n - keep_from].copy_(key[keep_from:])
+        self._slots_v[at:at + n - keep_from].copy_(value[keep_from:])
+        self._fill = stream - spilled
+        self._written += n
 
     def write(self, key: torch.Tensor, value: torch.Tensor,
               num_tokens: int) -> Optional[tuple[torch.Tensor, torch.Tensor]]:
-        """Append tokens; when the ring is full and more arrive, its whole
-        content is returned as overflow and the ring restarts (smaq/capture.py:60-91)."""
-        spill_k, spill_v = [], []
-        done = 0
-        while done < num_tokens:
-            if self._pos >= self.capacity:
-                spill_k.append(self._k[: self._pos].clone())
-                spill_v.append(self._v[: self._pos].clone())
-                self._pos = 0
-            n = min(num_tokens - done, self.capacity - self._pos)
-            self._k[self._pos: self._pos + n] = key[done: done + n]
-            self._v[self._pos: self._pos + n] = value[done: done + n]
-            self._pos += n
-            done += n
-        self._total_written += num_tokens
-        if spill_k:
-            return torch.cat(spill_k, dim=0), torch.cat(spill_v, dim=0)
-        return None
+        """Append tokens; returns the overflow (its own tensors) when the ring
+        wrapped, else None (smaq/capture.py:60-91)."""
+        out: list[tuple[torch.Tensor, torch.Tensor]] = []
+
+        def keep(pieces: Pieces) -> None:
+            out.append((torch.cat([k for k, _ in pieces]), torch.cat([v for _, v in pieces])))
+
+        self._advance(key, value, num_tokens, keep)
+        return out[0] if out else None
 
     def drain(self) -> Optional[tuple[torch.Tensor, torch.Tensor]]:
-        if self._pos == 0:
+        """The buffered tokens (copies); the ring is left empty."""
+        if self._fill == 0:
             return None
-        k, v = self._k[: self._pos].clone(), self._v[: self._pos].clone()
-        self._pos = 0
+        k, v = self._slots_k[:self._fill].clone(), self._slots_v[:self._fill].clone()
+        self._fill = 0
         return k, v
 
     def peek(self) -> Optional[tuple[torch.Tensor, torch.Tensor]]:
-        if self._pos == 0:
+        """Views of the buffered tokens, oldest first."""
+        if self._fill == 0:
             return None
-        return self._k[: self._pos], self._v[: self._pos]
+        return self._slots_k[:self._fill], self._slots_v[:self._fill]
 
     def reset(self):
-        self._pos = 0
-        self._total_written = 0
+        self._fill = 0
+        self._written = 0
 
 
 class KVCaptureEngine:
@@ -103,37 +137,47 @@ class KVCaptureEngine:
         return self.total_compressed_tokens + self.total_buffered_tokens
 
     def ingest_prefill(self, key: torch.Tensor, value: torch.Tensor, num_tokens: int):
-        """All but the last ``capacity`` tokens go to the store
-        (smaq/capture.py:145-153); like the reference, a write that overflows a
-        partly filled ring drops that overflow."""
-        if num_tokens <= self.ring.capacity:
-            self.ring.write(key[:num_tokens], value[:num_tokens], num_tokens)
-        else:
-            n_c = num_tokens - self.ring.capacity
-            self.store.append_chunk(key[:n_c], value[:n_c])
-            self.ring.write(key[n_c:num_tokens], value[n_c:num_tokens], self.ring.capacity)
+        """The newest ``capacity`` tokens go to the ring, the older ones to the
+        store (smaq/capture.py:145-153).  As in the reference, a spill caused
+        by writing into a partly filled ring is dropped, not stored."""
+        C = self.ring.capacity
+        head = max(0, num_tokens - C)
+        if head:
+            self.store.append_chunk(key[:head], value[:head])
+        self.ring._advance(key[head:num_tokens], value[head:num_tokens], num_tokens - head, None)
         self._prefill_done = True
 
     def ingest_prefill_from_paged_cache(self, kv_cache_tensor: torch.Tensor, num_tokens: int,
                                         block_table: torch.Tensor, block_size: int):
-        """Gather a prefill from a vLLM paged KV tensor [2, blocks, bs, Hkv, D]
-        (smaq/capture.py:155-177)."""
-        nblk = (num_tokens + block_size - 1) // block_size
+        """A prefill read out of a vLLM paged KV tensor [2, blocks, block_size,
+        Hkv, D] through the sequence's block table (smaq/capture.py:155-177):
+        one gather of the needed blocks, then ``ingest_prefill``."""
+        nblk = -(-num_tokens // block_size)
         phys = block_table[:nblk].to(kv_cache_tensor.device, torch.long)
-        k = kv_cache_tensor[0].index_select(0, phys).reshape(-1, *kv_cache_tensor.shape[3:])[:num_tokens]
-        v = kv_cache_tensor[1].index_select(0, phys).reshape(-1, *kv_cache_tensor.shape[3:])[:num_tokens]
-        self.ingest_prefill(k, v, num_tokens)
+        kv = kv_cache_tensor.index_select(1, phys)                   # [2, nblk, bs, Hkv, D]
+        kv = kv.reshape(2, nblk * block_size, *kv_cache_tensor.shape[3:])[:, :num_tokens]
+        self.ingest_prefill(kv[0], kv[1], num_tokens)
+
+    def _to_store(self, pieces: Pieces) -> None:
+        """One chunk given as pieces: in place for a store that takes pieces,
+        else joined for a store with only the reference's ``append_chunk``."""
+        append_parts = getattr(self.store, "append_parts", None)
+        if append_parts is not None:
+            append_parts(pieces)
+        else:
+            self.store.append_chunk(torch.cat([k for k, _ in pieces]), torch.cat([v for _, v in pieces]))
 
     def ingest_decode(self, key: torch.Tensor, value: torch.Tensor, num_tokens: int):
-        """(smaq/capture.py:179-183)"""
-        overflow = self.ring.write(key[:num_tokens], value[:num_tokens], num_tokens)
-        if overflow is not None:
-            self.store.append_chunk(*overflow)
+        """Decode tokens into the ring; a spill is encoded into the store
+        directly from the ring's slots and the new tokens (smaq/capture.py:179-183)."""
+        self.ring._advance(key, value, num_tokens, self._to_store)
 
     def flush(self):
-        data = self.ring.drain()
-        if data is not None:
-            self.store.append_chunk(*data)
+        """Move the buffered tokens into the store (smaq/capture.py:185-189)."""
+        pieces = self.ring.peek()
+        if pieces is not None:
+            self._to_store([pieces])
+            self.ring._fill = 0
 
     def reset(self):
         self.ring.reset()

@@ -94,7 +94,7 @@ __global__ __launch_bounds__(kVqThreads) void encode_blockvq_kernel(
         }
       }
       if (!seen_nan && second <= best * (1.0f + 2e-6f)) ++ties;
-      idx_out[row * nb + b] = (uint8_t)best_i;
+      idx_out[map.out_row(row) * nb + b] = (uint8_t)best_i;
     }
   }
   add_count(tie_count, ties);
@@ -119,7 +119,7 @@ __global__ __launch_bounds__(256) void dequant_blockvq_kernel(const uint8_t* __r
 using namespace smaq;
 
 extern "C" int smaq_encode_blockvq(const void* k, int kdtype, long long n_outer, long long n_inner,
-                                   long long s_outer, long long s_inner, int n_blocks,
+                                   long long s_outer, long long s_inner, long long out_outer, int n_blocks,
                                    int block_dim, int n_centroids, const float* E_blocks,
                                    const float* centroids, void* idx_out,
                                    unsigned long long* tie_count, void* stream) {
@@ -133,9 +133,11 @@ extern "C" int smaq_encode_blockvq(const void* k, int kdtype, long long n_outer,
                "smaq_encode_blockvq: codebook too large (%d blocks x %d centroids)", n_blocks,
                n_centroids);
   SMAQ_REQUIRE(n_outer >= 0 && n_inner > 0, "smaq_encode_blockvq: bad row shape");
+  SMAQ_REQUIRE(out_outer == 0 || out_outer >= n_inner, "smaq_encode_blockvq: output rows overlap "
+               "(out_outer %lld < n_inner %lld)", out_outer, n_inner);
   const int64_t rows = (int64_t)n_outer * n_inner;
   if (rows == 0) return SMAQ_OK;
-  RowMap map{n_inner, s_outer, s_inner};
+  RowMap map{n_inner, s_outer, s_inner, out_outer ? out_outer : n_inner};
   hipStream_t st = (hipStream_t)stream;
   if (encode_blockvq_mfma_supported(n_blocks, block_dim, n_centroids, k, kdtype, s_outer, s_inner))
     return launch_encode_blockvq_mfma(kdtype, k, map, rows, n_blocks, E_blocks, centroids,

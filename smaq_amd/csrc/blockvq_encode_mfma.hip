@@ -274,6 +274,7 @@ __global__ __launch_bounds__(kVmThreads) void encode_blockvq_mfma_kernel(
   for (; tile < n_tiles; tile += stride) {
     const int64_t row = tile * 16 + n;
     const bool valid = row < rows;
+    uint8_t* const out = idx_out + map.out_row(valid ? row : 0) * nb;
     const T* const kr_next = key_row(tile + stride);
     for (int b = 0; b < nb; ++b) {
       float kv[kVmBd];
@@ -370,7 +371,7 @@ __global__ __launch_bounds__(kVmThreads) void encode_blockvq_mfma_kernel(
         if (n == t0) idx = ci;
         if (lane == t0) ties += tie ? 1u : 0u;
       }
-      if (valid && kg == 0) idx_out[row * nb + b] = (uint8_t)idx;
+      if (valid && kg == 0) out[b] = (uint8_t)idx;
     }
     kr = kr_next;
   }

@@ -78,7 +78,7 @@ __global__ __launch_bounds__(kEncThreads) void encode_scalar_kernel(
         for (int d = main_end; d < D; ++d) b = fmaf(xs[r][d], xs[r][d], b);
       }
       const float n = Num<T>::round(sqrtf(b));
-      norms_out[r0 + r] = Num<T>::from_f(n);
+      norms_out[map.out_row(r0 + r)] = Num<T>::from_f(n);
       nprime[r] = Num<T>::round(n + 1e-10f);
     }
     __syncthreads();
@@ -119,7 +119,7 @@ __global__ __launch_bounds__(kEncThreads) void encode_scalar_kernel(
         const int d = p * vpb + e;
         if (d < D) byte += (uint32_t)cs[r][d] << (e * bits);
       }
-      codes_out[(r0 + r) * P + p] = (uint8_t)byte;
+      codes_out[map.out_row(r0 + r) * P + p] = (uint8_t)byte;
     }
     __syncthreads();
   }
@@ -321,7 +321,8 @@ static int launch_scores(const float* qrot, int64_t batch, int64_t nq, int64_t N
 using namespace smaq;
 
 extern "C" int smaq_encode_scalar(const void* k, int kdtype, long long n_outer, long long n_inner,
-                                  long long s_outer, long long s_inner, int D, const float* Mt,
+                                  long long s_outer, long long s_inner, long long out_outer, int D,
+                                  const float* Mt,
                                   const float* coord_scales, const float* bounds, int n_bounds,
                                   int bits, void* codes_out, void* norms_out,
                                   unsigned long long* tie_count, void* stream) {
@@ -332,9 +333,11 @@ extern "C" int smaq_encode_scalar(const void* k, int kdtype, long long n_outer, 
   SMAQ_REQUIRE(n_bounds >= 0 && n_bounds <= kMaxBounds && n_bounds < 256,
                "smaq_encode_scalar: %d decision boundaries unsupported", n_bounds);
   SMAQ_REQUIRE(n_outer >= 0 && n_inner > 0, "smaq_encode_scalar: bad row shape");
+  SMAQ_REQUIRE(out_outer == 0 || out_outer >= n_inner, "smaq_encode_scalar: output rows overlap "
+               "(out_outer %lld < n_inner %lld)", out_outer, n_inner);
   const int64_t rows = (int64_t)n_outer * n_inner;
   if (rows == 0) return SMAQ_OK;
-  RowMap map{n_inner, s_outer, s_inner};
+  RowMap map{n_inner, s_outer, s_inner, out_outer ? out_outer : n_inner};
   hipStream_t st = (hipStream_t)stream;
   if (encode_scalar_mfma_supported(D, bits, n_bounds, codes_out, k, kdtype, s_outer, s_inner))
     return launch_encode_scalar_mfma(kdtype, k, map, rows, Mt, coord_scales, bounds, n_bounds, bits,

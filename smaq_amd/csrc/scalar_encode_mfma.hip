@@ -173,7 +173,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if (!kSequentialNorm)
         for (int l = 1; l < 8; ++l) b = b + part[tid][l];
       const float nn = Num<T>::round(sqrtf(b));
-      if (tid < nr) norms_out[r0 + tid] = Num<T>::from_f(nn);
+      if (tid < nr) norms_out[map.out_row(r0 + tid)] = Num<T>::from_f(nn);
       nprime[tid] = Num<T>::round(nn + 1e-10f);
     }
     __syncthreads();
@@ -270,7 +270,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       // dword [c0 c1 c2 c3] folds into packed bytes with one dot product
       constexpr int nbytes = P / 4;
       const uint32_t* src = (const uint32_t*)&cs[lr][32 * lq];
-      uint8_t* dst = codes_out + (r0 + lr) * P + lq * nbytes;
+      uint8_t* dst = codes_out + map.out_row(r0 + lr) * P + lq * nbytes;
       uint32_t wds[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
       for (int q = 0; q < 8; ++q) {

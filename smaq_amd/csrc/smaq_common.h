@@ -65,13 +65,20 @@ __device__ __forceinline__ float round_half_even(float x) { return __builtin_rin
 // Row addressing shared by the encoders: logical row r = o * n_inner + i lives
 // at element offset o * s_outer + i * s_inner; its last dim is contiguous.
 // This covers both contiguous [rows, D] input and the [T, Hkv, D] -> [Hkv, T]
-// transpose view that the store hands to the codecs.
+// transpose view that the store hands to the codecs.  Its outputs go to
+// output row o * out_outer + i: dense (r itself) when out_outer == n_inner,
+// or the tail rows of per-head columns [Hkv, capacity, ...] when out_outer is
+// the columns' capacity (the store's encode-on-append).
 struct RowMap {
-  int64_t n_inner, s_outer, s_inner;
+  int64_t n_inner, s_outer, s_inner, out_outer;
   __device__ __forceinline__ int64_t offset(int64_t r) const {
     const int64_t o = r / n_inner;
     const int64_t i = r - o * n_inner;
     return o * s_outer + i * s_inner;
+  }
+  __device__ __forceinline__ int64_t out_row(int64_t r) const {
+    if (out_outer == n_inner) return r;
+    return r + (r / n_inner) * (out_outer - n_inner);
   }
 };
 

@@ -35,6 +35,7 @@ __global__ __launch_bounds__(256) void pack_values_kernel(
   const int64_t row = unit / units_per_row;
   const int g0 = (int)(unit - row * units_per_row) * groups_per_thread;
   const T* src = v + map.offset(row);
+  const int64_t orow = map.out_row(row);
   const int vpb = value_codes_per_byte(bits);
   const int row_bytes = D / vpb;
   const float levels = (float)((1 << bits) - 1);
@@ -53,8 +54,8 @@ __global__ __launch_bounds__(256) void pack_values_kernel(
     }
     float sc = Num<T>::round(Num<T>::round(hi - lo) / levels);
     if (sc < min_scale) sc = min_scale;  // clamp(min=1e-10), NaN passes
-    scales[row * n_groups + g] = Num<T>::from_f(sc);
-    zeros[row * n_groups + g] = Num<T>::from_f(lo);
+    scales[orow * n_groups + g] = Num<T>::from_f(sc);
+    zeros[orow * n_groups + g] = Num<T>::from_f(lo);
     for (int e = 0; e < group; ++e) {
       const float x = Num<T>::to_f(gp[e]);
       float q = round_half_even(Num<T>::round(Num<T>::round(x - lo) / sc));
@@ -63,7 +64,7 @@ __global__ __launch_bounds__(256) void pack_values_kernel(
       acc |= code << (filled * bits);
       if (++filled == vpb) {
         const int d = g * group + e;
-        data[row * row_bytes + d / vpb] = (uint8_t)acc;
+        data[orow * row_bytes + d / vpb] = (uint8_t)acc;
         acc = 0;
         filled = 0;
       }
@@ -86,6 +87,7 @@ __global__ __launch_bounds__(256) void pack_values_g32_kernel(
   const int64_t row = n_groups == 4 ? unit >> 2 : unit / n_groups;
   const int g = (int)(unit - row * n_groups);
   const T* gp = v + map.offset(row) + g * kG;
+  const int64_t orow = map.out_row(row);
   const float min_scale = dtype_const<T>(1e-10f);
 
   float x[kG];
@@ -110,8 +112,8 @@ __global__ __launch_bounds__(256) void pack_values_g32_kernel(
   }
   float sc = Num<T>::round(Num<T>::round(hi - lo) / levels);
   if (sc < min_scale) sc = min_scale;  // clamp(min=1e-10), NaN passes
-  scales[row * n_groups + g] = Num<T>::from_f(sc);
-  zeros[row * n_groups + g] = Num<T>::from_f(lo);
+  scales[orow * n_groups + g] = Num<T>::from_f(sc);
+  zeros[orow * n_groups + g] = Num<T>::from_f(lo);
   uint32_t out[4] = {0u, 0u, 0u, 0u};
   if constexpr (std::is_same<T, bf16>::value) {
     // bf16: a / sc as a * RN(1 / sc), with the roundings to bf16 done by the
@@ -139,7 +141,7 @@ __global__ __launch_bounds__(256) void pack_values_g32_kernel(
       out[e / (4 * vpb)] |= code << (BITS * (e % (4 * vpb)));
     }
   }
-  uint8_t* dst = data + row * (n_groups * kG / vpb) + g * (kG / vpb);
+  uint8_t* dst = data + orow * (n_groups * kG / vpb) + g * (kG / vpb);
   if constexpr (BITS == 2) *(uint2*)dst = uint2{out[0], out[1]};
   else *(uint4*)dst = uint4{out[0], out[1], out[2], out[3]};
 }
@@ -207,8 +209,9 @@ static int launch_dequant(const void* data, const void* scales, const void* zero
 using namespace smaq;
 
 extern "C" int smaq_pack_values(const void* v, int vdtype, long long n_outer, long long n_inner,
-                                long long s_outer, long long s_inner, int D, int bits, int group,
-                                void* data_out, void* scales_out, void* zeros_out, void* stream) {
+                                long long s_outer, long long s_inner, long long out_outer, int D,
+                                int bits, int group, void* data_out, void* scales_out, void* zeros_out,
+                                void* stream) {
   SMAQ_REQUIRE(v && data_out && scales_out && zeros_out, "smaq_pack_values: null pointer");
   SMAQ_REQUIRE(D > 0 && group > 0 && D % group == 0,
                "head_dim %d must be divisible by group_size %d", D, group);
@@ -220,7 +223,9 @@ extern "C" int smaq_pack_values(const void* v, int vdtype, long long n_outer, lo
   const int64_t rows = (int64_t)n_outer * n_inner;
   if (rows == 0) return SMAQ_OK;
   SMAQ_REQUIRE(rows * (D / group) < (1ll << 40), "smaq_pack_values: too many rows");
-  RowMap map{n_inner, s_outer, s_inner};
+  SMAQ_REQUIRE(out_outer == 0 || out_outer >= n_inner, "smaq_pack_values: output rows overlap "
+               "(out_outer %lld < n_inner %lld)", out_outer, n_inner);
+  RowMap map{n_inner, s_outer, s_inner, out_outer ? out_outer : n_inner};
   hipStream_t st = (hipStream_t)stream;
   switch (vdtype) {
     case SMAQ_F32: return launch_pack<float>(v, map, rows, D, bits, group, data_out, scales_out, zeros_out, st);

@@ -1,62 +1,84 @@
-"""Value codec and the standalone SMAQ KV cache (drop-in for smaq/kv_cache.py).
+"""Value codec re-exports and the standalone SMAQ KV cache (drop-in for
+smaq/kv_cache.py).
 
-``quantize_values`` is the value bit-packer (HIP kernel): per group of
-``group_size`` elements, asymmetric min/max quantisation to ``bits`` bits,
-2-bit codes packed four per byte and 4-bit codes two per byte.
-``dequantize_values`` is its HIP inverse.
+``SMAQKVCache`` keeps the newest ``buffer_size`` tokens of a ``[..., T, D]``
+key/value stream exact and the older ones compressed.  Its compressed part is
+a ``ColumnHistory`` (one lane per leading index, e.g. batch x head): a flush
+encodes the tokens leaving the exact window straight into the columns' tail
+rows.  The exact window lives in a buffer twice its size in which tokens
+occupy a sliding range: appends write at the end, flushes advance the start,
+and the range is moved to the front only when the end reaches the buffer's
+capacity -- a copy of ``buffer_size`` tokens once per ``buffer_size``
+appended tokens.  (The reference concatenates the whole exact buffer on every
+append and the whole compressed history on every flush,
+smaq/kv_cache.py:176-216.)
 """
 
 from __future__ import annotations
 
 import math
-from typing import Any, NamedTuple, Optional
+from typing import Any, Optional
 
 import torch
 
-from smaq_amd import _native
 from smaq_amd.calibration import IdentityCalibrationProvider
+from smaq_amd.columns import ColumnHistory, codec_kind
 from smaq_amd.core import CacheCapabilities, CalibrationProvider
 from smaq_amd.quantizer import default_device
 from smaq_amd.strategies import SMAQFullMetricScalarStrategy
+from smaq_amd.value_codec import (ValueQuantized, dequantize_values, quantize_values,  # noqa: F401
+                                  unpack_values)
 
 
-class ValueQuantized(NamedTuple):
-    """Bit-packed values (smaq/kv_cache.py:20-26)."""
+class _ExactWindow:
+    """The newest tokens of a [*lead, T, D] stream, in order, as a view of a
+    buffer of twice the window size."""
 
-    data: torch.Tensor
-    scales: torch.Tensor
-    zeros: torch.Tensor
-    bits: int = 2
+    def __init__(self):
+        self.k: Optional[torch.Tensor] = None
+        self.v: Optional[torch.Tensor] = None
+        self.start = self.end = 0
 
+    @property
+    def size(self) -> int:
+        return self.end - self.start
 
-def unpack_values(vq: ValueQuantized) -> torch.Tensor:
-    """Per-element uint8 codes from packed bytes (smaq/kv_cache.py:29-47)."""
-    bits = vq.bits if len(vq) > 3 else 2
-    p = vq.data
-    if bits == 2:
-        return torch.stack([p & 0x03, (p >> 2) & 0x03, (p >> 4) & 0x03, (p >> 6) & 0x03],
-                           dim=-1).reshape(*p.shape[:-1], p.shape[-1] * 4)
-    if bits == 4:
-        return torch.stack([p & 0x0F, (p >> 4) & 0x0F], dim=-1).reshape(*p.shape[:-1], p.shape[-1] * 2)
-    return p
+    def views(self):
+        if self.k is None or self.size == 0:
+            return None, None
+        return self.k[..., self.start:self.end, :], self.v[..., self.start:self.end, :]
 
+    def push(self, key: torch.Tensor, value: torch.Tensor, window: int) -> None:
+        t = key.shape[-2]
+        if self.k is None:
+            cap = max(2 * window, t)
+            self.k = key.new_empty(*key.shape[:-2], cap, key.shape[-1])
+            self.v = value.new_empty(*value.shape[:-2], cap, value.shape[-1])
+        elif key.shape[:-2] != self.k.shape[:-2] or key.shape[-1] != self.k.shape[-1]:
+            raise ValueError(f"appended keys {tuple(key.shape)} do not continue the cache's "
+                             f"{tuple(self.k.shape[:-2])} x {self.k.shape[-1]} stream")
+        if key.dtype != self.k.dtype or value.dtype != self.v.dtype:
+            # widen, as concatenating tensors of two float dtypes does
+            self.k = self.k.to(torch.promote_types(self.k.dtype, key.dtype))
+            self.v = self.v.to(torch.promote_types(self.v.dtype, value.dtype))
+        if self.end + t > self.k.shape[-2]:
+            n = self.size
+            cap = max(self.k.shape[-2], n + t)
+            k2 = self.k.new_empty(*self.k.shape[:-2], cap, self.k.shape[-1])
+            v2 = self.v.new_empty(*self.v.shape[:-2], cap, self.v.shape[-1])
+            k2[..., :n, :].copy_(self.k[..., self.start:self.end, :])
+            v2[..., :n, :].copy_(self.v[..., self.start:self.end, :])
+            self.k, self.v, self.start, self.end = k2, v2, 0, n
+        self.k[..., self.end:self.end + t, :].copy_(key)
+        self.v[..., self.end:self.end + t, :].copy_(value)
+        self.end += t
 
-def quantize_values(v: torch.Tensor, bits: int = 2, group_size: int = 32) -> ValueQuantized:
-    """Groupwise asymmetric quantisation (smaq/kv_cache.py:50-91), HIP kernel."""
-    data, scales, zeros = _native.pack_values(v, bits, group_size)
-    return ValueQuantized(data=data, scales=scales, zeros=zeros, bits=bits)
-
-
-def dequantize_values(vq: ValueQuantized, group_size: int = 32) -> torch.Tensor:
-    """fp32 code * scale + zero (smaq/kv_cache.py:94-103), HIP kernel."""
-    bits = vq.bits if len(vq) > 3 else 2
-    return _native.dequant_values(vq.data, vq.scales, vq.zeros, bits, group_size)
-
-
-def _cat_value_q(a: ValueQuantized, b: ValueQuantized, bits: int) -> ValueQuantized:
-    return ValueQuantized(data=torch.cat([a.data, b.data], dim=-2),
-                          scales=torch.cat([a.scales, b.scales], dim=-2),
-                          zeros=torch.cat([a.zeros, b.zeros], dim=-2), bits=bits)
+    def pop_front(self, n: int):
+        """Views of the oldest n tokens; they leave the window (the views stay
+        valid until the next push)."""
+        k, v = self.k[..., self.start:self.start + n, :], self.v[..., self.start:self.start + n, :]
+        self.start += n
+        return k, v
 
 
 class SMAQKVCache:
@@ -86,110 +108,151 @@ class SMAQKVCache:
         self.dtype = dtype
         self.layer_idx = layer_idx
         self.calibration_provider = calibration_provider or IdentityCalibrationProvider()
-        sigma = Sigma_q
-        if sigma is None:
-            sigma = self.calibration_provider.get_sigma_q(layer_idx, head_dim, device=self.device)
-        self.key_quantizer = key_strategy or SMAQFullMetricScalarStrategy(
-            dim=head_dim, Sigma_q=sigma, bits=key_bits, device=self.device, dtype=torch.float32)
+        if key_strategy is None:
+            sigma = Sigma_q if Sigma_q is not None else self.calibration_provider.get_sigma_q(
+                layer_idx, head_dim, device=self.device)
+            key_strategy = SMAQFullMetricScalarStrategy(dim=head_dim, Sigma_q=sigma, bits=key_bits,
+                                                        device=self.device, dtype=torch.float32)
+        self.key_quantizer = key_strategy
         self.seq_len = 0
-        self.key_quantized: Optional[Any] = None
-        self.value_quantized: Optional[ValueQuantized] = None
-        self.key_buffer: Optional[torch.Tensor] = None
-        self.value_buffer: Optional[torch.Tensor] = None
+        self._lead: Optional[tuple[int, ...]] = None
+        self._hist: Optional[ColumnHistory] = None
+        # strategies without a column encoder keep quantised chunks
+        self._chunks: list[tuple[Any, ValueQuantized]] = []
+        self._joined: Optional[tuple[Any, ValueQuantized]] = None
+        self._exact = _ExactWindow()
 
     @property
     def capabilities(self) -> CacheCapabilities:
         return self.key_quantizer.capabilities
 
-    def prefill(self, keys: torch.Tensor, values: torch.Tensor):
-        """Keep the last ``buffer_size`` tokens exact, compress the rest
-        (smaq/kv_cache.py:154-174)."""
-        seq_len = keys.shape[-2]
-        self.seq_len = seq_len
-        if seq_len <= self.buffer_size:
-            self.key_buffer, self.value_buffer = keys, values
+    # -- compressed history ------------------------------------------------
+    @property
+    def key_quantized(self):
+        if self._hist is not None:
+            return self._hist.key_quantized(self._lead)
+        joined = self._join()
+        return None if joined is None else joined[0]
+
+    @property
+    def value_quantized(self) -> Optional[ValueQuantized]:
+        if self._hist is not None:
+            return self._hist.value_quantized(self._lead)
+        joined = self._join()
+        return None if joined is None else joined[1]
+
+    def _join(self):
+        if not self._chunks:
+            return None
+        if self._joined is None:
+            ks = [k for k, _ in self._chunks]
+            vs = [v for _, v in self._chunks]
+            key_q = ks[0] if len(ks) == 1 else self.key_quantizer.concat_quantized(ks)
+            val_q = vs[0] if len(vs) == 1 else ValueQuantized(
+                data=torch.cat([v.data for v in vs], dim=-2), scales=torch.cat([v.scales for v in vs], dim=-2),
+                zeros=torch.cat([v.zeros for v in vs], dim=-2), bits=self.value_bits)
+            self._joined = (key_q, val_q)
+        return self._joined
+
+    def _compress(self, keys: torch.Tensor, values: torch.Tensor) -> None:
+        """Append [*lead, n, D] tokens to the compressed history."""
+        if keys.shape[-2] == 0:
             return
-        nq = seq_len - self.buffer_size
-        self.key_buffer, self.value_buffer = keys[..., nq:, :], values[..., nq:, :]
-        self.key_quantized = self.key_quantizer.quantize(keys[..., :nq, :])
-        self.value_quantized = quantize_values(values[..., :nq, :], bits=self.value_bits,
-                                               group_size=self.value_group_size)
+        lead = tuple(keys.shape[:-2])
+        if self._lead is None:
+            self._lead = lead
+        elif lead != self._lead:
+            raise ValueError(f"keys with leading shape {lead} do not continue the cache's {self._lead}")
+        if self._hist is None and not self._chunks and codec_kind(self.key_quantizer) is not None:
+            lanes = math.prod(lead) if lead else 1
+            self._hist = ColumnHistory(self.key_quantizer, lanes, self.head_dim, self.value_bits,
+                                       self.value_group_size, self.device)
+        if self._hist is not None:
+            d = keys.shape[-1]
+            self._hist.append([(keys.reshape(-1, keys.shape[-2], d), values.reshape(-1, values.shape[-2], d))])
+        else:
+            self._chunks.append((self.key_quantizer.quantize(keys),
+                                 quantize_values(values, bits=self.value_bits, group_size=self.value_group_size)))
+            self._joined = None
+
+    # -- exact window --------------------------------------------------------
+    @property
+    def key_buffer(self) -> Optional[torch.Tensor]:
+        return self._exact.views()[0]
+
+    @property
+    def value_buffer(self) -> Optional[torch.Tensor]:
+        return self._exact.views()[1]
+
+    # -- cache protocol (smaq/kv_cache.py:154-290) -------------------------
+    def prefill(self, keys: torch.Tensor, values: torch.Tensor):
+        """Compress all but the newest ``buffer_size`` tokens, keep those exact
+        (smaq/kv_cache.py:154-174)."""
+        n = keys.shape[-2]
+        self.seq_len = n
+        n_old = max(0, n - self.buffer_size)
+        # a prefill replaces the exact window, and the compressed history too
+        # when it compresses tokens (the reference assigns both)
+        self._exact = _ExactWindow()
+        if n_old:
+            self._lead, self._hist, self._chunks, self._joined = None, None, [], None
+        self._compress(keys[..., :n_old, :], values[..., :n_old, :])
+        self._exact.push(keys[..., n_old:, :], values[..., n_old:, :], self.buffer_size)
 
     def append(self, key: torch.Tensor, value: torch.Tensor):
-        """(smaq/kv_cache.py:176-188)"""
+        """Add tokens to the exact window; whatever no longer fits in
+        ``buffer_size`` is compressed (smaq/kv_cache.py:176-216)."""
         self.seq_len += key.shape[-2]
-        if self.key_buffer is not None:
-            self.key_buffer = torch.cat([self.key_buffer, key], dim=-2)
-            self.value_buffer = torch.cat([self.value_buffer, value], dim=-2)
-        else:
-            self.key_buffer, self.value_buffer = key, value
-        if self.key_buffer.shape[-2] > self.buffer_size:
-            self._flush_buffer()
-
-    def _flush_buffer(self):
-        """(smaq/kv_cache.py:190-216)"""
-        nf = self.key_buffer.shape[-2] - self.buffer_size
-        kf, vf = self.key_buffer[..., :nf, :], self.value_buffer[..., :nf, :]
-        self.key_buffer, self.value_buffer = self.key_buffer[..., nf:, :], self.value_buffer[..., nf:, :]
-        new_k = self.key_quantizer.quantize(kf)
-        new_v = quantize_values(vf, bits=self.value_bits, group_size=self.value_group_size)
-        if self.key_quantized is None:
-            self.key_quantized, self.value_quantized = new_k, new_v
-            return
-        self.key_quantized = self.key_quantizer.concat_quantized([self.key_quantized, new_k])
-        self.value_quantized = _cat_value_q(self.value_quantized, new_v, self.value_bits)
+        self._exact.push(key, value, self.buffer_size)
+        over = self._exact.size - self.buffer_size
+        if over > 0:
+            self._compress(*self._exact.pop_front(over))
 
     def attention_scores(self, query: torch.Tensor, scale: float | None = None) -> torch.Tensor:
-        """[compressed scores, exact scores] along the key axis, no softmax
+        """[compressed, exact] scores along the key axis, no softmax
         (smaq/kv_cache.py:218-241)."""
         if scale is None:
             scale = 1.0 / math.sqrt(self.head_dim)
         parts = []
-        if self.key_quantized is not None:
-            if getattr(self.key_quantizer, "supports_kernel", False):
-                parts.append(self.key_quantizer.attention_score(query, self.key_quantized, scale=scale,
-                                                                use_kernel=True))
-            else:
-                parts.append(self.key_quantizer.attention_score(query, self.key_quantized, scale=scale))
-        if self.key_buffer is not None:
+        kq = self.key_quantized
+        if kq is not None:
+            kw = {"use_kernel": True} if getattr(self.key_quantizer, "supports_kernel", False) else {}
+            parts.append(self.key_quantizer.attention_score(query, kq, scale=scale, **kw))
+        kb = self.key_buffer
+        if kb is not None:
             # (a contiguous right operand: batched bf16 products of a transposed view are avoided)
-            parts.append(torch.matmul(query, self.key_buffer.transpose(-2, -1).contiguous()) * scale)
+            parts.append(torch.matmul(query, kb.transpose(-2, -1).contiguous()) * scale)
         if not parts:
-            return torch.empty(*query.shape[:-2], query.shape[-2], 0, device=query.device, dtype=query.dtype)
+            return query.new_empty(*query.shape[:-2], query.shape[-2], 0)
         return torch.cat(parts, dim=-1)
 
     def attend(self, attn_weights: torch.Tensor) -> torch.Tensor:
-        """Weights over [compressed, exact] applied to the values
-        (smaq/kv_cache.py:243-267)."""
-        outs = []
+        """Weights over [compressed, exact] applied to the dequantised and the
+        exact values (smaq/kv_cache.py:243-267)."""
+        out = None
         col = 0
-        if self.value_quantized is not None:
-            nq = self.value_quantized.data.shape[-2]
-            v_hat = dequantize_values(self.value_quantized, self.value_group_size)
-            outs.append(torch.matmul(attn_weights[..., col:col + nq], v_hat))
+        vq = self.value_quantized
+        if vq is not None:
+            nq = vq.data.shape[-2]
+            out = torch.matmul(attn_weights[..., col:col + nq], dequantize_values(vq, self.value_group_size))
             col += nq
-        if self.value_buffer is not None:
-            nb = self.value_buffer.shape[-2]
-            outs.append(torch.matmul(attn_weights[..., col:col + nb], self.value_buffer))
-        if not outs:
-            return torch.zeros(*attn_weights.shape[:-1], self.head_dim, device=attn_weights.device,
-                               dtype=attn_weights.dtype)
-        return sum(outs)
+        vb = self.value_buffer
+        if vb is not None:
+            part = torch.matmul(attn_weights[..., col:col + vb.shape[-2]], vb)
+            out = part if out is None else out + part
+        if out is None:
+            return attn_weights.new_zeros(*attn_weights.shape[:-1], self.head_dim)
+        return out
 
     def memory_bytes(self) -> dict[str, int]:
-        """Byte accounting with 16-bit metadata (smaq/kv_cache.py:269-287)."""
-        info = {"quantized_keys": 0, "quantized_values": 0, "buffer": 0, "total": 0}
-        if self.key_quantized is not None:
-            info["quantized_keys"] += self.key_quantizer.memory_bytes(self.key_quantized)
-        if self.value_quantized is not None:
-            vq = self.value_quantized
-            info["quantized_values"] += vq.data.nelement() + vq.scales.nelement() * 2 + vq.zeros.nelement() * 2
-        if self.key_buffer is not None:
-            info["buffer"] += self.key_buffer.nelement() * 2
-        if self.value_buffer is not None:
-            info["buffer"] += self.value_buffer.nelement() * 2
-        info["total"] = info["quantized_keys"] + info["quantized_values"] + info["buffer"]
-        return info
+        """Byte accounting with 16-bit metadata and 2-byte exact elements
+        (smaq/kv_cache.py:269-287)."""
+        kq, vq = self.key_quantized, self.value_quantized
+        keys = self.key_quantizer.memory_bytes(kq) if kq is not None else 0
+        vals = 0 if vq is None else vq.data.nelement() + 2 * vq.scales.nelement() + 2 * vq.zeros.nelement()
+        kb, vb = self.key_buffer, self.value_buffer
+        buf = 0 if kb is None else 2 * (kb.nelement() + vb.nelement())
+        return {"quantized_keys": keys, "quantized_values": vals, "buffer": buf, "total": keys + vals + buf}
 
     def get_seq_length(self) -> int:
         return self.seq_len

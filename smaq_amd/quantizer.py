@@ -143,6 +143,12 @@ class SMAQQuantizer(torch.nn.Module):
                                              self.bits, ties=self.tie_counter)
         return SMAQQuantized(indices=codes, norms=norms, bits=self.bits)
 
+    def encode_into(self, k: torch.Tensor, codes: torch.Tensor, norms: torch.Tensor) -> None:
+        """``quantize`` of k [lanes, T, dim] written into column views
+        codes [lanes, T, P], norms [lanes, T] (append-only storage)."""
+        _native.encode_scalar(k, self.E.float().t().contiguous(), self.decision_boundaries, self.bits,
+                              ties=self.tie_counter, out=(codes, norms))
+
     def dequantize(self, q: SMAQQuantized) -> torch.Tensor:
         """((c[code] @ E_inv^T) * norm) as E.dtype (smaq/quantizer.py:147-152)."""
         return _native.dequant_scalar(q.indices, q.norms, q.bits, self.dim, self.centroids,

@@ -1,26 +1,29 @@
 """Compressed KV store (drop-in for smaq/store.py).
 
-History is quantised chunk by chunk on append (key strategy + value packer,
-both HIP kernels) and exposed as a head-major ``FlatCache``: per KV head,
-key codes [N, P], norms [N], value bytes [N, D/vpb], scales and zeros
-[N, D/group] -- the layout the fused attention kernel streams.
-
-Appends write into preallocated, geometrically grown GPU buffers, so a new
-chunk costs a copy of that chunk only (the reference re-concatenates the
-whole history on the first read after every append, smaq/store.py:97-114).
+History is exposed as a head-major ``FlatCache``: per KV head, key codes
+[N, P], norms [N], value bytes [N, D/vpb], scales and zeros [N, D/group] --
+the layout the fused attention kernel streams.  For the GPU codecs (scalar
+SMAQ / rotation scalar / block-VQ keys) the fields are append-only columns
+(``smaq_amd.columns.ColumnHistory``): an appended chunk is encoded by the HIP
+kernels straight into the columns' next rows and ``get_flat_cache`` returns
+views of the filled rows, so an append costs the encode of that chunk only.
+(The reference quantises each chunk into its own tensors and concatenates
+all of them on the first read after every append, smaq/store.py:83-114.)
+Other strategies keep the reference's list of quantised chunks.
 """
 
 from __future__ import annotations
 
-from typing import Any, NamedTuple, Optional
+from typing import Any, NamedTuple, Optional, Sequence
 
 import torch
 
 from smaq_amd.calibration import IdentityCalibrationProvider
+from smaq_amd.columns import ColumnHistory, codec_kind
 from smaq_amd.core import CacheCapabilities, CalibrationProvider
-from smaq_amd.kv_cache import ValueQuantized, quantize_values
 from smaq_amd.quantizer import default_device
 from smaq_amd.strategies import SMAQFullMetricScalarStrategy
+from smaq_amd.value_codec import ValueQuantized, quantize_values
 
 
 class FlatCache(NamedTuple):
@@ -29,27 +32,6 @@ class FlatCache(NamedTuple):
     key_q: Any
     value_q: ValueQuantized
     num_tokens: int
-
-
-class _Column:
-    """One per-token tensor field stored [Hkv, capacity, *tail], grown x2."""
-
-    def __init__(self):
-        self.buf: Optional[torch.Tensor] = None
-
-    def append(self, chunk: torch.Tensor, n_old: int) -> None:
-        # chunk [Hkv, T, *tail]
-        n_new = n_old + chunk.shape[1]
-        if self.buf is None or self.buf.shape[1] < n_new:
-            cap = max(n_new, 2 * (0 if self.buf is None else self.buf.shape[1]), 256)
-            grown = torch.empty((chunk.shape[0], cap, *chunk.shape[2:]), dtype=chunk.dtype, device=chunk.device)
-            if self.buf is not None and n_old:
-                grown[:, :n_old].copy_(self.buf[:, :n_old])
-            self.buf = grown
-        self.buf[:, n_old:n_new].copy_(chunk)
-
-    def view(self, n: int) -> torch.Tensor:
-        return self.buf[:, :n]
 
 
 class CompressedKVStore:
@@ -76,21 +58,18 @@ class CompressedKVStore:
         self.device = torch.device(device) if device is not None else default_device()
         self.layer_idx = layer_idx
         self.calibration_provider = calibration_provider or IdentityCalibrationProvider()
-        sigma = Sigma_q
-        if sigma is None:
-            sigma = self.calibration_provider.get_sigma_q(layer_idx, head_dim, device=self.device)
-        self.key_strategy = key_strategy or SMAQFullMetricScalarStrategy(
-            dim=head_dim, Sigma_q=sigma, bits=key_bits, device=self.device, dtype=torch.float32)
+        if key_strategy is None:
+            sigma = Sigma_q if Sigma_q is not None else self.calibration_provider.get_sigma_q(
+                layer_idx, head_dim, device=self.device)
+            key_strategy = SMAQFullMetricScalarStrategy(dim=head_dim, Sigma_q=sigma, bits=key_bits,
+                                                        device=self.device, dtype=torch.float32)
+        self.key_strategy = key_strategy
         self.quantizer = self.key_strategy
-        self._key_chunks: list[Any] = []
-        self._value_chunks: list[ValueQuantized] = []
-        self._chunk_lengths: list[int] = []
-        self._flat: Optional[FlatCache] = None
-        # append-only GPU columns (used for strategies with fused kernels)
-        self._cols: dict[str, _Column] = {}
-        self._n = 0
-        self._key_meta: Optional[tuple] = None
+        self._lengths: list[int] = []
+        self._hist: Optional[ColumnHistory] = None
+        self._chunks: list[tuple[Any, ValueQuantized]] = []
         self._mem_bytes = 0
+        self._flat: Optional[FlatCache] = None
 
     @property
     def capabilities(self) -> CacheCapabilities:
@@ -98,113 +77,72 @@ class CompressedKVStore:
 
     @property
     def num_tokens(self) -> int:
-        return sum(self._chunk_lengths)
+        return sum(self._lengths)
 
     @property
     def num_chunks(self) -> int:
-        return len(self._chunk_lengths)
+        return len(self._lengths)
 
     def append_chunk(self, key: torch.Tensor, value: torch.Tensor):
         """Quantise and append a [T, Hkv, D] chunk (smaq/store.py:83-95)."""
-        chunk_len = key.shape[0]
-        k = key.transpose(0, 1).unsqueeze(0)
-        v = value.transpose(0, 1).unsqueeze(0)
-        key_q = self.key_strategy.quantize(k)
-        val_q = quantize_values(v, bits=self.value_bits, group_size=self.value_group_size)
-        self._mem_bytes += self.key_strategy.memory_bytes(key_q) + _value_bytes(val_q)
-        self._chunk_lengths.append(chunk_len)
-        if self._append_columns(key_q, val_q):
-            # the columns hold the chunk; the chunk tensors are released
-            self._key_chunks.clear()
-            self._value_chunks.clear()
-        else:
-            self._key_chunks.append(key_q)
-            self._value_chunks.append(val_q)
-        self._flat = None
+        self.append_parts([(key, value)])
 
-    def _append_columns(self, key_q: Any, val_q: ValueQuantized) -> bool:
-        """Copy the chunk into the columns; False (columns dropped) for key
-        layouts they do not handle."""
-        fields = _key_fields(key_q)
-        if fields is None or (self._n and not self._cols):
-            if self._cols:
-                raise ValueError("key chunks of different layouts in one store")
-            return False
-        meta, tensors = fields
-        if self._key_meta is not None and self._key_meta != meta:
-            raise ValueError("key chunks of different layouts in one store")
-        self._key_meta = meta
-        tensors = dict(tensors)
-        tensors["v_data"] = val_q.data.reshape(-1, *val_q.data.shape[-2:])
-        tensors["v_scales"] = val_q.scales.reshape(-1, *val_q.scales.shape[-2:])
-        tensors["v_zeros"] = val_q.zeros.reshape(-1, *val_q.zeros.shape[-2:])
-        n_old = self._n
-        for name, t in tensors.items():
-            self._cols.setdefault(name, _Column()).append(t, n_old)
-        self._n = n_old + tensors["v_data"].shape[1]
-        return True
+    def append_parts(self, parts: Sequence[tuple[torch.Tensor, torch.Tensor]]):
+        """Append one chunk given as consecutive [T_i, Hkv, D] pieces -- a ring
+        flush hands over the ring's exact tokens followed by the new ones
+        without joining them first.  Same result as ``append_chunk`` of their
+        concatenation."""
+        T = sum(k.shape[0] for k, _ in parts)
+        if self._hist is None and not self._chunks and codec_kind(self.key_strategy) is not None:
+            self._hist = ColumnHistory(self.key_strategy, self.num_kv_heads, self.head_dim, self.value_bits,
+                                       self.value_group_size, self.device)
+        if self._hist is not None:
+            # [T, Hkv, D] -> [Hkv, T, D] views: every head is one lane of rows
+            self._mem_bytes += self._hist.append([(k.transpose(0, 1), v.transpose(0, 1)) for k, v in parts])
+        else:
+            key = parts[0][0] if len(parts) == 1 else torch.cat([k for k, _ in parts])
+            value = parts[0][1] if len(parts) == 1 else torch.cat([v for _, v in parts])
+            k = key.transpose(0, 1).unsqueeze(0)
+            v = value.transpose(0, 1).unsqueeze(0)
+            key_q = self.key_strategy.quantize(k)
+            val_q = quantize_values(v, bits=self.value_bits, group_size=self.value_group_size)
+            self._chunks.append((key_q, val_q))
+            self._mem_bytes += self.key_strategy.memory_bytes(key_q) + _value_bytes(val_q)
+        self._lengths.append(T)
+        self._flat = None
 
     def get_flat_cache(self) -> Optional[FlatCache]:
         """Head-major flattened history (smaq/store.py:97-114)."""
-        if not self._chunk_lengths:
+        if not self._lengths:
             return None
         if self._flat is not None:
             return self._flat
-        n = self._n
-        if self._cols and self._key_meta is not None:
-            kind, bits_or_nb, block_dim = self._key_meta
-            if kind == "scalar":
-                from smaq_amd.quantizer import SMAQQuantized
-                key_q = SMAQQuantized(indices=self._cols["k_codes"].view(n), norms=self._cols["k_norms"].view(n),
-                                      bits=bits_or_nb)
-            else:
-                from smaq_amd.block_vq import BlockVQQuantized
-                key_q = BlockVQQuantized(indices=self._cols["k_codes"].view(n), n_blocks=bits_or_nb,
-                                         block_dim=block_dim)
-            vq = ValueQuantized(data=self._cols["v_data"].view(n), scales=self._cols["v_scales"].view(n),
-                                zeros=self._cols["v_zeros"].view(n), bits=self.value_bits)
+        if self._hist is not None:
+            if self._hist.n == 0:
+                return None
+            key_q, vq = self._hist.key_quantized(), self._hist.value_quantized()
         else:
             s = self.key_strategy
-            if len(self._key_chunks) == 1:
-                key_q = s.flatten_quantized(self._key_chunks[0])
-                vq = _flatten_value_q(self._value_chunks[0])
+            flat = [(s.flatten_quantized(k), _flatten_value_q(v)) for k, v in self._chunks]
+            if len(flat) == 1:
+                key_q, vq = flat[0]
             else:
-                key_q = s.concat_quantized([s.flatten_quantized(c) for c in self._key_chunks])
-                vq = _concat_value_q([_flatten_value_q(c) for c in self._value_chunks])
+                key_q = s.concat_quantized([k for k, _ in flat])
+                vq = _concat_value_q([v for _, v in flat])
         self._flat = FlatCache(key_q=key_q, value_q=vq, num_tokens=self.num_tokens)
         return self._flat
 
     def memory_bytes(self) -> int:
-        """Per-chunk key bytes plus value bytes with 16-bit metadata, summed
-        over the appended chunks (smaq/store.py:116-124)."""
+        """Key strategy bytes plus value bytes with 16-bit metadata, summed over
+        the appended chunks (smaq/store.py:116-124)."""
         return self._mem_bytes
 
     def reset(self):
-        self._key_chunks.clear()
-        self._value_chunks.clear()
-        self._chunk_lengths.clear()
-        self._flat = None
-        self._cols = {}
-        self._n = 0
-        self._key_meta = None
+        self._lengths.clear()
+        self._hist = None
+        self._chunks.clear()
         self._mem_bytes = 0
-
-
-def _key_fields(key_q: Any):
-    """Per-token key tensors of a quantised chunk as [Hkv, T, ...] views, or
-    None for layouts the columns do not handle."""
-    from smaq_amd.block_vq import BlockVQQuantized
-    from smaq_amd.quantizer import SMAQQuantized
-    if isinstance(key_q, SMAQQuantized):
-        ind = key_q.indices
-        return ("scalar", key_q.bits, 0), {
-            "k_codes": ind.reshape(-1, *ind.shape[-2:]),
-            "k_norms": key_q.norms.reshape(-1, key_q.norms.shape[-1]),
-        }
-    if isinstance(key_q, BlockVQQuantized):
-        ind = key_q.indices
-        return ("block_vq", key_q.n_blocks, key_q.block_dim), {"k_codes": ind.reshape(-1, *ind.shape[-2:])}
-    return None
+        self._flat = None
 
 
 def _value_bytes(vq: ValueQuantized) -> int:
@@ -215,17 +153,10 @@ def _value_bytes(vq: ValueQuantized) -> int:
 def _flatten_value_q(value_q: ValueQuantized) -> ValueQuantized:
     """(1, H, T, ...) -> (H, T, ...) (smaq/store.py:133-141)."""
     bits = value_q.bits if len(value_q) > 3 else 2
-    return ValueQuantized(
-        data=value_q.data.reshape(-1, value_q.data.shape[-2], value_q.data.shape[-1]).contiguous(),
-        scales=value_q.scales.reshape(-1, value_q.scales.shape[-2], value_q.scales.shape[-1]).contiguous(),
-        zeros=value_q.zeros.reshape(-1, value_q.zeros.shape[-2], value_q.zeros.shape[-1]).contiguous(),
-        bits=bits,
-    )
+    return ValueQuantized(*(t.reshape(-1, *t.shape[-2:]).contiguous() for t in value_q[:3]), bits=bits)
 
 
 def _concat_value_q(chunks: list[ValueQuantized]) -> ValueQuantized:
     """Token-dim concatenation (smaq/store.py:144-152)."""
     bits = chunks[0].bits if len(chunks[0]) > 3 else 2
-    return ValueQuantized(data=torch.cat([c.data for c in chunks], dim=-2),
-                          scales=torch.cat([c.scales for c in chunks], dim=-2),
-                          zeros=torch.cat([c.zeros for c in chunks], dim=-2), bits=bits)
+    return ValueQuantized(*(torch.cat([c[i] for c in chunks], dim=-2) for i in range(3)), bits=bits)

@@ -172,6 +172,12 @@ class RotationAdapter(torch.nn.Module):
                                              self.bits, coord_scales=self.coord_scales, ties=self.tie_counter)
         return SMAQQuantized(indices=codes, norms=norms, bits=self.bits)
 
+    def encode_into(self, k: torch.Tensor, codes: torch.Tensor, norms: torch.Tensor) -> None:
+        """``quantize`` of k [lanes, T, dim] written into column views
+        codes [lanes, T, P], norms [lanes, T] (append-only storage)."""
+        _native.encode_scalar(k, self.rotation.float().t().contiguous(), self.decision_boundaries, self.bits,
+                              coord_scales=self.coord_scales, ties=self.tie_counter, out=(codes, norms))
+
     def dequantize(self, q: SMAQQuantized) -> torch.Tensor:
         """(c[code] * (1/s)) @ R * norm (smaq/weighted_scalar.py:357-363)."""
         return _native.dequant_scalar(q.indices, q.norms, q.bits, self.dim, self.centroids,

@@ -40,19 +40,19 @@ def test_library_exports_every_declared_symbol():
 def test_status_codes_map_to_exceptions():
     lib = _native.lib()
     # null pointers: rejected before any device call
-    st = lib.smaq_pack_values(None, 0, 1, 1, 0, 0, 128, 2, 32, None, None, None, None)
+    st = lib.smaq_pack_values(None, 0, 1, 1, 0, 0, 0, 128, 2, 32, None, None, None, None)
     assert st == -1
     assert b"null pointer" in lib.smaq_last_error()
     with pytest.raises(ValueError, match="null pointer"):
         _native._check(st, "smaq_pack_values")
     dummy = ctypes.c_void_p(16)
-    st = lib.smaq_pack_values(dummy, 0, 1, 1, 0, 0, 100, 2, 32, dummy, dummy, dummy, None)
+    st = lib.smaq_pack_values(dummy, 0, 1, 1, 0, 0, 0, 100, 2, 32, dummy, dummy, dummy, None)
     assert st == -1 and b"divisible by group_size" in lib.smaq_last_error()
-    st = lib.smaq_encode_blockvq(dummy, 0, 1, 1, 0, 0, 16, 8, 512, dummy, dummy, dummy, None, None)
+    st = lib.smaq_encode_blockvq(dummy, 0, 1, 1, 0, 0, 0, 16, 8, 512, dummy, dummy, dummy, None, None)
     assert st == -1 and b"n_centroids" in lib.smaq_last_error()
-    st = lib.smaq_encode_scalar(dummy, 0, 1, 1, 0, 0, 512, dummy, None, dummy, 7, 3, dummy, dummy, None, None)
+    st = lib.smaq_encode_scalar(dummy, 0, 1, 1, 0, 0, 0, 512, dummy, None, dummy, 7, 3, dummy, dummy, None, None)
     assert st == -1 and b"head_dim" in lib.smaq_last_error()
-    st = lib.smaq_pack_values(dummy, 7, 1, 1, 0, 0, 128, 2, 32, dummy, dummy, dummy, None)
+    st = lib.smaq_pack_values(dummy, 7, 1, 1, 0, 0, 0, 128, 2, 32, dummy, dummy, dummy, None)
     assert st == -2
     with pytest.raises(RuntimeError):
         _native._check(st, "smaq_pack_values")
@@ -138,6 +138,30 @@ def test_ring_buffer_matches_oracle():
         assert (pa is None) == (pb is None)
         if pa is not None:
             assert torch.equal(pa[0], pb[0])
+    assert ring.total_written == ref.total
+
+
+@pytest.mark.parametrize("cap", [1, 3, 8])
+def test_ring_buffer_spill_arithmetic(cap):
+    """Random write sizes (empty, single, several capacities at once, writes
+    into a full ring) against the oracle's slot-by-slot restatement; inputs
+    in another dtype spill in the ring's dtype, as writing them into the
+    slots first would."""
+    g = torch.Generator().manual_seed(cap)
+    ring = S.RingBuffer(cap, 2, 4, device=torch.device("cpu"), dtype=torch.bfloat16)
+    ref = R.Ring(cap, 2, 4, dtype=torch.bfloat16)
+    for step in range(60):
+        n = int(torch.randint(0, 3 * cap + 2, (1,), generator=g))
+        x = torch.randn(max(n, 1), 2, 4, generator=g)           # fp32 input
+        a, b = ring.write(x, 2 * x, n), ref.write(x, 2 * x, n)
+        assert (a is None) == (b is None), step
+        if a is not None:
+            assert a[0].dtype == torch.bfloat16
+            assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1]), step
+        pa, pb = ring.peek(), ref.peek()
+        assert (pa is None) == (pb is None), step
+        if pa is not None:
+            assert torch.equal(pa[0], pb[0]) and torch.equal(pa[1], pb[1]), step
     assert ring.total_written == ref.total
 
 

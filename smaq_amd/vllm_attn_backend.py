@@ -1,14 +1,28 @@
 """Legacy vLLM entry point (drop-in for smaq/vllm_attn_backend.py).
 
-Maps the legacy modes onto the adapter's (shadow and accumulate capture only,
-active serves hybrid decode) and forwards to ``smaq_amd.integration.vllm``.
+The legacy API names three modes: ``shadow`` and ``accumulate`` capture K/V
+into the compressed store while vLLM keeps serving attention, ``active``
+serves decode steps from the store (hybrid attention).  They map onto the
+adapter's capture-only and hybrid modes (``smaq_amd.integration.vllm``),
+which does all the work; this module keeps the legacy names, the module-wide
+current mode, and the no-alloc start-up hook.
+
+No-alloc start-up: ``enable_no_alloc`` records a configuration and, when
+vLLM is importable, wraps two of its methods once per process --
+``Executor.get_kv_cache_specs`` first installs the hooks (active, no_alloc)
+on every worker through the executor's ``collective_rpc`` and then sizes the
+KV cache as before; ``GPUModelRunner._update_hybrid_attention_mamba_layout``
+first gives layers that share another layer's KV cache that layer's entry.
+Without vLLM it logs a warning and does nothing else.
 """
 
 from __future__ import annotations
 
+import functools
 import logging
+from typing import Any, Callable, Optional
 
-import smaq_amd.integration.vllm as _backend
+import smaq_amd.integration.vllm as _adapter
 
 logger = logging.getLogger("smaq_amd.attn")
 
@@ -17,23 +31,23 @@ MODE_ACCUMULATE = "accumulate"
 MODE_ACTIVE = "active"
 _VALID_MODES = (MODE_SHADOW, MODE_ACCUMULATE, MODE_ACTIVE)
 
-_LEGACY_TO_NEW = {
-    MODE_SHADOW: _backend.MODE_CAPTURE_ONLY,
-    MODE_ACCUMULATE: _backend.MODE_CAPTURE_ONLY,
-    MODE_ACTIVE: _backend.MODE_HYBRID,
-}
+# legacy mode -> what the adapter does in it
+_ADAPTER_MODE = {MODE_SHADOW: _adapter.MODE_CAPTURE_ONLY,
+                 MODE_ACCUMULATE: _adapter.MODE_CAPTURE_ONLY,
+                 MODE_ACTIVE: _adapter.MODE_HYBRID}
 
 _GLOBAL_MODE = MODE_ACCUMULATE
-_SMAQ_NO_ALLOC_CONFIG = None
+# the configuration enable_no_alloc recorded (None until it is called)
+_SMAQ_NO_ALLOC_CONFIG: Optional[dict] = None
 
 
 def set_mode(mode: str) -> None:
-    """(smaq/vllm_attn_backend.py:31-36)"""
+    """Switch every installed layer's behaviour (smaq/vllm_attn_backend.py:31-36)."""
     global _GLOBAL_MODE
-    if mode not in _VALID_MODES:
+    if mode not in _ADAPTER_MODE:
         raise ValueError(f"Invalid mode: {mode}. Valid: {_VALID_MODES}")
+    _adapter.set_mode(_ADAPTER_MODE[mode])
     _GLOBAL_MODE = mode
-    _backend.set_mode(_LEGACY_TO_NEW[mode])
 
 
 def get_mode() -> str:
@@ -44,76 +58,85 @@ def install_smaq_hooks(model_runner, calibration_covariances=None, key_bits: int
                        value_group_size: int = 32, buffer_size: int = 128, initial_layers_count: int = 4,
                        initial_layers_key_bits: int | None = None, mode: str = MODE_ACCUMULATE,
                        no_alloc: bool = False, paged: bool = False):
-    """Install the adapter's hooks under a legacy mode
-    (smaq/vllm_attn_backend.py:43-75); ``paged`` is the adapter's paged-pool
+    """Hook every attention layer of ``model_runner`` (smaq/vllm_attn_backend.py:43-75).
+
+    ``buffer_size`` is the exact recent window (the capture ring's capacity);
+    an unknown ``mode`` installs capture-only hooks.  The layer states are
+    returned and kept on the runner (``_smaq_states``), with the no-alloc
+    flag (``_smaq_no_alloc``).  ``paged`` is the adapter's paged-pool
     extension."""
     global _GLOBAL_MODE
-    states = _backend.install_hooks(
-        model_runner, calibration_covariances=calibration_covariances, key_bits=key_bits, value_bits=value_bits,
-        value_group_size=value_group_size, ring_capacity=buffer_size, initial_layers_count=initial_layers_count,
-        initial_layers_key_bits=initial_layers_key_bits, mode=_LEGACY_TO_NEW.get(mode, _backend.MODE_CAPTURE_ONLY),
-        no_alloc=no_alloc, paged=paged)
-    _GLOBAL_MODE = mode
+    states = _adapter.install_hooks(
+        model_runner, calibration_covariances=calibration_covariances, key_bits=key_bits,
+        value_bits=value_bits, value_group_size=value_group_size, ring_capacity=buffer_size,
+        initial_layers_count=initial_layers_count, initial_layers_key_bits=initial_layers_key_bits,
+        mode=_ADAPTER_MODE.get(mode, _adapter.MODE_CAPTURE_ONLY), no_alloc=no_alloc, paged=paged)
     model_runner._smaq_states = states
     model_runner._smaq_no_alloc = no_alloc
+    _GLOBAL_MODE = mode
     return states
+
+
+def _wrap_once(cls: Any, method: str, marker: str, make: Callable[[Callable], Callable]) -> None:
+    """Replace cls.method by make(original), once per class (``marker`` flags it)."""
+    if getattr(cls, marker, False):
+        return
+    setattr(cls, method, make(getattr(cls, method)))
+    setattr(cls, marker, True)
+
+
+def _install_on_worker(cfg: dict, worker) -> dict:
+    """Runs inside each vLLM worker (via collective_rpc): hooks from the
+    configuration it was sent, serving from the store, vLLM's KV cache unused.
+    The configuration travels with the call (bound by functools.partial), so
+    workers in other processes see it too."""
+    states = install_smaq_hooks(worker.model_runner, mode=MODE_ACTIVE, no_alloc=True, **cfg)
+    return {"hooks": len(states)}
+
+
+def _specs_after_install(original: Callable) -> Callable:
+    def get_kv_cache_specs(self):
+        cfg = _SMAQ_NO_ALLOC_CONFIG
+        if cfg is not None:
+            try:
+                self.collective_rpc(functools.partial(_install_on_worker, dict(cfg)))
+            except Exception as exc:   # workers keep vLLM's own attention
+                logger.exception("[SMAQ] collective_rpc failed during no-alloc install: %s", exc)
+        return original(self)
+    return get_kv_cache_specs
+
+
+def _layout_with_shared_layers(original: Callable) -> Callable:
+    def update_layout(self, kv_caches):
+        for layer, owner in getattr(self, "shared_kv_cache_layers", {}).items():
+            if layer not in kv_caches and owner in kv_caches:
+                kv_caches[layer] = kv_caches[owner]
+        return original(self, kv_caches)
+    return update_layout
 
 
 def enable_no_alloc(calibration_covariances=None, key_bits: int = 3, value_bits: int = 2, buffer_size: int = 128,
                     initial_layers_count: int = 4):
     """Have vLLM install the hooks (active, no_alloc) on every worker while
-    it sizes its KV cache (smaq/vllm_attn_backend.py:78-149).  Inert, with a
-    warning, when vLLM is not importable."""
+    it sizes its KV cache (smaq/vllm_attn_backend.py:78-149)."""
     global _SMAQ_NO_ALLOC_CONFIG
-    _SMAQ_NO_ALLOC_CONFIG = dict(calibration_covariances=calibration_covariances, key_bits=key_bits,
-                                 value_bits=value_bits, buffer_size=buffer_size,
-                                 initial_layers_count=initial_layers_count)
+    _SMAQ_NO_ALLOC_CONFIG = {"calibration_covariances": calibration_covariances, "key_bits": key_bits,
+                             "value_bits": value_bits, "buffer_size": buffer_size,
+                             "initial_layers_count": initial_layers_count}
     try:
         from vllm.v1.executor.abstract import Executor
         from vllm.v1.worker.gpu_model_runner import GPUModelRunner
     except ImportError:
         logger.warning("[SMAQ] vLLM is not installed; enable_no_alloc is inert.")
         return
-    if hasattr(Executor, "_smaq_patched"):
+    if getattr(Executor, "_smaq_patched", False):
         return
-    if not hasattr(GPUModelRunner, "_smaq_layout_patch"):
-        orig_layout = GPUModelRunner._update_hybrid_attention_mamba_layout
-
-        def layout_update(self, kv_caches):
-            # layers that share another layer's cache get that cache's entry
-            for name, target in getattr(self, "shared_kv_cache_layers", {}).items():
-                if name not in kv_caches and target in kv_caches:
-                    kv_caches[name] = kv_caches[target]
-            return orig_layout(self, kv_caches)
-
-        GPUModelRunner._update_hybrid_attention_mamba_layout = layout_update
-        GPUModelRunner._smaq_layout_patch = True
-    orig_specs = Executor.get_kv_cache_specs
-
-    def get_kv_cache_specs(self):
-        cfg = _SMAQ_NO_ALLOC_CONFIG
-        if cfg is None:
-            return orig_specs(self)
-
-        def install_on_worker(worker):
-            states = install_smaq_hooks(worker.model_runner, calibration_covariances=cfg["calibration_covariances"],
-                                        key_bits=cfg["key_bits"], value_bits=cfg["value_bits"],
-                                        buffer_size=cfg["buffer_size"],
-                                        initial_layers_count=cfg["initial_layers_count"], mode=MODE_ACTIVE,
-                                        no_alloc=True)
-            return {"hooks": len(states)}
-
-        try:
-            self.collective_rpc(install_on_worker)
-        except Exception as exc:  # a worker without a model runner keeps vLLM's own path
-            logger.exception("[SMAQ] collective_rpc failed during no-alloc install: %s", exc)
-        return orig_specs(self)
-
-    Executor.get_kv_cache_specs = get_kv_cache_specs
-    Executor._smaq_patched = True
+    _wrap_once(GPUModelRunner, "_update_hybrid_attention_mamba_layout", "_smaq_layout_patch",
+               _layout_with_shared_layers)
+    _wrap_once(Executor, "get_kv_cache_specs", "_smaq_patched", _specs_after_install)
     logger.info("[SMAQ] Patched Executor for automatic no-alloc hook installation")
 
 
 def free_kv_cache(model_runner):
-    """(smaq/vllm_attn_backend.py:152-154)"""
-    return _backend.free_kv_cache(model_runner)
+    """Release vLLM's paged KV cache of the hooked layers (smaq/vllm_attn_backend.py:152-154)."""
+    return _adapter.free_kv_cache(model_runner)

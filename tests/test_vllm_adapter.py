@@ -239,3 +239,58 @@ def test_paged_layer_geometry_checks():
     # MLA layers never get pools
     runner2 = make_runner({"mla": FakeMLAImpl()}, CPU)
     assert I.install_hooks(runner2, paged=True)["mla"].paged is None
+
+
+def test_enable_no_alloc_patches_fake_vllm(monkeypatch):
+    """With (fake) vLLM importable: the executor's KV-cache sizing first
+    installs active no-alloc hooks on every worker through collective_rpc
+    (the call is picklable, carrying the recorded configuration), the runner's
+    layout update maps shared-cache layers, and patching happens once."""
+    import pickle
+    import sys
+    import types
+
+    class Executor:
+        def __init__(self, workers):
+            self.workers, self.rpc_calls = workers, 0
+
+        def collective_rpc(self, fn):
+            self.rpc_calls += 1
+            fn = pickle.loads(pickle.dumps(fn))      # what a multi-process executor does
+            return [fn(w) for w in self.workers]
+
+        def get_kv_cache_specs(self):
+            return "specs"
+
+    class GPUModelRunner:
+        def _update_hybrid_attention_mamba_layout(self, kv_caches):
+            return sorted(kv_caches)
+
+    mods = {"vllm": types.ModuleType("vllm"), "vllm.v1": types.ModuleType("vllm.v1"),
+            "vllm.v1.executor": types.ModuleType("vllm.v1.executor"),
+            "vllm.v1.executor.abstract": types.ModuleType("vllm.v1.executor.abstract"),
+            "vllm.v1.worker": types.ModuleType("vllm.v1.worker"),
+            "vllm.v1.worker.gpu_model_runner": types.ModuleType("vllm.v1.worker.gpu_model_runner")}
+    mods["vllm.v1.executor.abstract"].Executor = Executor
+    mods["vllm.v1.worker.gpu_model_runner"].GPUModelRunner = GPUModelRunner
+    for name, mod in mods.items():
+        monkeypatch.setitem(sys.modules, name, mod)
+    monkeypatch.setattr(LB, "_SMAQ_NO_ALLOC_CONFIG", None)
+
+    runner, _ = _runner(n_layers=2)
+    worker = types.SimpleNamespace(model_runner=runner)
+    ex = Executor([worker])
+    assert ex.get_kv_cache_specs() == "specs" and ex.rpc_calls == 0       # before enable: untouched
+    LB.enable_no_alloc(buffer_size=32, key_bits=4)
+    LB.enable_no_alloc(buffer_size=32, key_bits=4)                        # idempotent
+    assert Executor._smaq_patched and GPUModelRunner._smaq_layout_patch
+    assert ex.get_kv_cache_specs() == "specs" and ex.rpc_calls == 1
+    states = runner._smaq_states
+    assert len(states) == 2 and runner._smaq_no_alloc is True
+    st = next(iter(states.values()))
+    assert st.engine.ring.capacity == 32 and st.config.key_bits == 4
+    assert LB.get_mode() == LB.MODE_ACTIVE and V.get_mode() == V.MODE_HYBRID
+    gm = GPUModelRunner()
+    gm.shared_kv_cache_layers = {"b": "a", "c": "missing"}
+    caches = {"a": 1}
+    assert gm._update_hybrid_attention_mamba_layout(caches) == ["a", "b"] and caches["b"] == 1

@@ -6,14 +6,28 @@
 // sequential FMA chain over d, code = #boundaries below y.  Here the chain is
 // replaced by v_mfma_f32_16x16x32_bf16 over exact bf16 splits of u and of the
 // matrix (u: 1, 2 or 3 parts for bf16, fp16, fp32 keys; matrix: 3 parts), so
-// every product is exact and only the accumulation differs.  One MFMA rounds
-// its result once against partial sums bounded by S = sum_d |u_d m_dj|
-// (measured on gfx950: <= 10.4 * 2^-24 * S over 12 chained MFMAs), so the
-// MFMA value is within err = kErr * S of the exact chain with kErr =
-// 32 * 2^-24 (S itself comes from one more MFMA of |u| and |M| hi parts).
-// A code is final when every boundary is farther than err plus the tie
-// tolerance from y; otherwise y is recomputed with the exact sequential chain
-// and counted as the reference does (including the tie counter).
+// every product is exact and only the accumulation differs.
+//
+// Decision margin.  Let S = sum_d |u_d m_dj| (from one more MFMA of |u| and
+// the |M| hi parts; x 1.03 covers those truncated parts) and u = 2^-24.  The
+// code must be the one the reference's chain y_c gives, and the matrix-core
+// value y_m and y_c both differ from the exact sum y:
+//   * y_c: 128 fmaf steps, each one rounding of a partial sum whose
+//     magnitude is at most S, so |y_c - y| <= 128 u S;
+//   * y_m: a chain of N MFMAs per output (N = 12, 20, 24 for bf16, fp16,
+//     fp32 keys: 4 K-steps x the part products kept), each adding exact
+//     products to its accumulator with at most two roundings of a value
+//     bounded by S (the largest error measured on gfx950 over 12 chained
+//     MFMAs was 10.4 u S, below the one-rounding-per-MFMA 12 u S), so the
+//     accumulation adds at most 2 N u S;
+//   * the part products not formed (u part i x matrix part j with i + j >= 3;
+//     truncated bf16 parts satisfy |p1| < 2^-7 |x|, |p2| < 2^-14 |x|) sum to
+//     less than 2 * 2^-21 S = 16 u S for fp32 keys (pairs 1x2, 2x1, 2x2) and
+//     2^-21 S = 8 u S for fp16 keys (pair 1x2); bf16 keys form every pair.
+// Hence |y_m - y_c| <= (2 N + 128 + dropped) u S =: err.  A code is final when every
+// boundary is farther than err plus the tie tolerance from y_m; otherwise y
+// is recomputed with the exact sequential chain and counted as the reference
+// does (including the tie counter).
 //
 // Tile: 64 rows per workgroup iteration, 4 waves; wave w owns output columns
 // 32w .. 32w+31 and keeps its matrix parts in registers for the whole grid
@@ -33,12 +47,24 @@ constexpr int kTR = 64;        // rows per tile
 constexpr int kD = 128;        // head_dim served
 constexpr int kXS = 132;       // floats per row of the fp32 tile
 constexpr int kAR = 272;       // bytes per row of one bf16 A part (256 + 16 pad)
-// accumulation error bound factor (x 1.03 for the truncated |u|, |M| used for S)
-constexpr float kErr = 32.0f * 1.03f / 16777216.0f;
-
 template <typename T> struct UParts { static constexpr int n = 3; };       // fp32
 template <> struct UParts<bf16> { static constexpr int n = 1; };
 template <> struct UParts<_Float16> { static constexpr int n = 2; };
+
+// MFMAs chained into one output: 4 K-steps x the (u part, matrix part) pairs
+// with up + ep < 3 (the smaller products are not formed; see kDropped)
+template <int UP>
+constexpr int kChainedMfma = 4 * (UP == 1 ? 3 : (UP == 2 ? 5 : 6));
+
+// bound on the part products not formed, in units of 2^-24 S
+template <int UP>
+constexpr float kDropped = UP == 1 ? 0.0f : (UP == 2 ? 8.0f : 16.01f);
+
+// |y_m - y_c| / S bound: two roundings per chained MFMA, the products not
+// formed, one rounding per step of the reference's 128-step chain; x 1.03 for
+// the truncated parts in S
+template <int UP>
+constexpr float kErr = (2.0f * kChainedMfma<UP> + kDropped<UP> + 128.0f) * 1.03f / 16777216.0f;
 
 __device__ __forceinline__ uint32_t fbits(float x) { return __builtin_bit_cast(uint32_t, x); }
 __device__ __forceinline__ float bfloat(uint32_t b) { return __builtin_bit_cast(float, b); }
@@ -230,7 +256,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int v = 0; v < 4; ++v) {
           const int row = 16 * rb + 4 * kg + v;
           const float y = coord_scales ? acc[cb][v] * cscale : acc[cb][v];
-          const float err = (coord_scales ? sac[cb][v] * fabsf(cscale) : sac[cb][v]) * kErr;
+          const float err = (coord_scales ? sac[cb][v] * fabsf(cscale) : sac[cb][v]) * kErr<UP>;
           // band: err + 1e-6 * (|y| + err) + 1e-12 (with the +-1e-6 |b| in guard[])
           const float wband = fmaf(1e-6f, fabsf(y), fmaf(err, 1.000001f, 1e-12f));
           int c = 0;

@@ -427,3 +427,29 @@ def test_scalar_encode_near_boundaries(dev, bits):
     print(f"\n[near-boundary {bits}b] ties={n_ties} gpu={qz.tie_counter.value()}")
     assert qz.tie_counter.value() == n_ties
     assert torch.equal(got.norms.cpu(), ref.norms)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_scalar_encode_cancellation_matches_the_chain(dev, dtype):
+    """Keys and a metric built for heavy cancellation: every y_j is a sum of
+    128 terms whose partial sums reach ~100x |y_j|, so the reference chain's
+    own rounding (up to a few 2^-24 S) decides codes near decision
+    boundaries.  The encoder must reproduce the chain exactly: codes equal the
+    oracle's everywhere, ties included (every undecided coordinate is
+    recounted with the chain)."""
+    g = torch.Generator().manual_seed(7)
+    D, N = 128, 65536
+    sign = torch.cat([torch.ones(64), -torch.ones(64)])
+    M = (sign * 20.0) * (1.0 + 0.01 * torch.randn(D, D, generator=g))
+    k = ((1.0 + 0.1 * torch.randn(N, D, generator=g)) * 3.0).to(dtype)
+    qz = S.SMAQQuantizer(D, bits=4, device=dev, E=M, E_inv=torch.linalg.inv(M))
+    got = qz.quantize(k.to(dev))
+    _, _, db = R.scalar_tables(4)
+    ref = R.scalar_encode(k, M, db, 4)
+    y = R.scalar_y(k, M).double()
+    S_ = (k.float() / (k.float().norm(dim=-1, keepdim=True))).double().abs() @ M.double().abs().T
+    near = ((y[..., None] - db.double()).abs() < 128 * 2.0 ** -24 * S_[..., None]).any(-1)
+    print(f"\n[cancellation {dtype}] coordinates within the chain-error band of a boundary: {int(near.sum())}")
+    assert int(near.sum()) > 100          # the construction exercises the recount
+    assert torch.equal(got.indices.cpu(), ref.indices)
+    assert torch.equal(got.norms.cpu(), ref.norms)

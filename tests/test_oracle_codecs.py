@@ -302,3 +302,46 @@ def test_quantize_values_bf16_per_op_rounding():
     assert np.array_equal(q.data.numpy(), packed)
     assert np.array_equal(q.scales.float().numpy(), sc[..., 0])
     assert np.array_equal(q.zeros.float().numpy(), lo[..., 0])
+
+
+# ------------------------------------------- scalar encoder's error margin ---
+
+def _split_bf16_np(x: np.ndarray):
+    """The encoder's truncated bf16 split of fp32 values (x = p0 + p1 + p2)."""
+    x = x.astype(np.float32)
+    b0 = (x.view(np.uint32) & np.uint32(0xFFFF0000)).view(np.float32)
+    r1 = (x - b0).astype(np.float32)
+    b1 = (r1.view(np.uint32) & np.uint32(0xFFFF0000)).view(np.float32)
+    r2 = (r1 - b1).astype(np.float32)
+    b2 = (r2.view(np.uint32) & np.uint32(0xFFFF0000)).view(np.float32)
+    return b0, b1, b2
+
+
+def test_bf16_split_bounds_used_by_the_encoder_margin():
+    """x = p0 + p1 + p2 exactly, |p1| < 2^-7 |x|, |p2| < 2^-14 |x| (normal
+    range): the skipped cross products are below 2^-21 relative."""
+    g = np.random.default_rng(5)
+    x = (g.standard_normal(200000) * np.exp2(g.integers(-20, 20, 200000))).astype(np.float32)
+    p0, p1, p2 = _split_bf16_np(x)
+    assert np.array_equal(p0.astype(np.float64) + p1 + p2, x.astype(np.float64))
+    ax = np.abs(x.astype(np.float64))
+    assert np.all(np.abs(p1) < ax * 2.0 ** -7) and np.all(np.abs(p2) < ax * 2.0 ** -14)
+
+
+def test_reference_chain_error_within_128_roundings():
+    """The reference's y = u @ M^T (torch-CPU, one sequential FMA chain per
+    output) stays within 128 * 2^-24 * S of the exact sum, S = sum |u_d m_d|,
+    on inputs built for heavy cancellation (partial sums far above |y|), the
+    bound the matrix-core encoder's decision margin uses."""
+    g = torch.Generator().manual_seed(6)
+    D, N = 128, 4096
+    sign = torch.cat([torch.ones(64), -torch.ones(64)])
+    M = (sign * 20.0) * (1.0 + 0.01 * torch.randn(D, D, generator=g))       # rows: +A then -A
+    u = (1.0 + 0.1 * torch.randn(N, D, generator=g)) / D ** 0.5
+    y = (u @ M.T).double()
+    y64 = u.double() @ M.double().T
+    S = u.double().abs() @ M.double().abs().T
+    err = (y - y64).abs() / S
+    assert float(err.max()) <= 128 * 2.0 ** -24
+    # the construction does cancel: |y| is far below S
+    assert float((y64.abs() / S).median()) < 0.05

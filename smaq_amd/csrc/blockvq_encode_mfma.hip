@@ -84,6 +84,30 @@ __device__ __forceinline__ uint32_t min3_u32(uint32_t a, uint32_t b, uint32_t c)
   return r;
 }
 
+// The lanes l ^ 16 (X16) and l ^ 32 (X32) as VALU permutes: with both
+// operands x, v_permlane16_swap / v_permlane32_swap leave each lane the pair
+// {x[l], x[l ^ 16]} / {x[l], x[l ^ 32]} (in some order), which is all a
+// symmetric reduction (min, sum) needs -- no LDS round trip.
+struct LanePair {
+  uint32_t a, b;
+};
+__device__ __forceinline__ LanePair pair_x16(uint32_t x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+  return {r[0], r[1]};
+}
+__device__ __forceinline__ LanePair pair_x32(uint32_t x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  return {r[0], r[1]};
+}
+// (x[l] + x[l ^ 16]) + (x[l ^ 32] + x[l ^ 48]): the same value, bit for bit,
+// in all four lanes of a token (fp32 addition commutes)
+__device__ __forceinline__ float sum_kgroups(float x) {
+  const LanePair p = pair_x16(fbits(x));
+  const float s = bitsf(p.a) + bitsf(p.b);
+  const LanePair q = pair_x32(fbits(s));
+  return bitsf(q.a) + bitsf(q.b);
+}
+
 // Orders this wave's LDS writes before its later LDS reads of other lanes'
 // data (a wave-local exchange).
 __device__ __forceinline__ void wave_sync() {
@@ -301,8 +325,7 @@ __global__ __launch_bounds__(kVmThreads) void encode_blockvq_mfma_kernel(
       *(__attribute__((address_space(3))) uint32_t*)(lds3 + ys_tok + 4 * kg) = h16(yah) | (h16(ybh) << 16);
       *(__attribute__((address_space(3))) uint32_t*)(lds3 + ys_tok + 16 + 4 * kg) = h16(yal) | (h16(ybl) << 16);
       float sq = ok ? xa * xa + xb * xb : __builtin_nanf("");
-      sq += __shfl_xor(sq, 16, 64);
-      sq += __shfl_xor(sq, 32, 64);
+      sq = sum_kgroups(sq);
       const float delta = kDeltaRel * (sq + smax_all[b]);
       const float s2 = sg * sg;
       const float init = (sq + delta) * s2;  // |x|^2 + delta, scaled
@@ -316,13 +339,18 @@ __global__ __launch_bounds__(kVmThreads) void encode_blockvq_mfma_kernel(
       const f32x4 acc0 = {init, init, init, init};
       uint32_t best = 0xffffffffu, second = 0xffffffffu;
       // software pipelined: the product of tile t + 1 is issued before the
-      // keys of tile t are reduced
+      // keys of tile t are reduced, and the A operand of tile t + 3 is read
+      // then (two tiles of LDS latency covered)
+      u32x4 a_n1 = ap[16], a_n2 = ap[32];
       f32x4 acc_next = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, ap[0]), bv, acc0, 0, 0, 0);
 #pragma unroll
       for (int t = 0; t < 16; ++t) {
         const f32x4 acc = acc_next;
-        if (t + 1 < 16)
-          acc_next = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, ap[16 * (t + 1)]), bv, acc0, 0, 0, 0);
+        if (t + 1 < 16) {
+          acc_next = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a_n1), bv, acc0, 0, 0, 0);
+          a_n1 = a_n2;
+          if (t + 3 < 16) a_n2 = ap[16 * (t + 3)];
+        }
 #pragma unroll
         for (int i = 0; i < 4; i += 2) {
           // centroids 16t + 4kg + i, i + 1 of token n; low 6 bits = (t, i)
@@ -335,11 +363,11 @@ __global__ __launch_bounds__(kVmThreads) void encode_blockvq_mfma_kernel(
       // merge the four k-group lanes of each token
       uint32_t gbest = best, gsecond = second;
 #pragma unroll
-      for (int off = 16; off < 64; off <<= 1) {
-        const uint32_t ob = (uint32_t)__shfl_xor((int)gbest, off, 64);
-        const uint32_t os = (uint32_t)__shfl_xor((int)gsecond, off, 64);
-        gsecond = min(min(gsecond, os), max(gbest, ob));
-        gbest = min(gbest, ob);
+      for (int step = 0; step < 2; ++step) {  // lanes l ^ 16, then l ^ 32
+        const LanePair pb = step == 0 ? pair_x16(gbest) : pair_x32(gbest);
+        const LanePair ps = step == 0 ? pair_x16(gsecond) : pair_x32(gsecond);
+        gsecond = min3_u32(ps.a, ps.b, max(pb.a, pb.b));
+        gbest = min(pb.a, pb.b);
       }
       const float vb = bitsf(gbest & 0xffffffc0u), vs = bitsf(gsecond & 0xffffffc0u);
       // clear winner: the runner-up more than delta behind (keys are
@@ -348,8 +376,11 @@ __global__ __launch_bounds__(kVmThreads) void encode_blockvq_mfma_kernel(
                          delta_s < 3.0e38f;
       const int kw = best == gbest ? kg : 4;  // the lane holding the winner
       int kwin = kw;
-      kwin = min(kwin, __shfl_xor(kwin, 16, 64));
-      kwin = min(kwin, __shfl_xor(kwin, 32, 64));
+      {
+        const LanePair p = pair_x16((uint32_t)kwin);
+        const LanePair q = pair_x32(min(p.a, p.b));
+        kwin = (int)min(q.a, q.b);
+      }
       const int tag = (int)(gbest & 63u);
       int idx = 16 * (tag >> 2) + 4 * kwin + (tag & 3);
       // exact recount of the unclear tokens, one at a time by the whole wave

@@ -26,12 +26,19 @@
 // takes the reference's argmin and tie count.
 //
 // Layout: one persistent workgroup of 16 waves per CU holds the split
-// codebook in LDS (16-byte rows, conflict-free ds_read_b128); each wave
-// encodes 16 tokens at a time, block after block, with the next block's key
-// bytes in flight.  The running minimum keeps the distance bits with the low
-// 6 bits replaced by the centroid's position in the lane (tile, row), so one
-// v_min3_u32 tracks value and index of two distances (distances are positive:
-// delta is added to every one) and a v_med3_u32 / v_min_u32 pair the runner-up.
+// codebook in LDS (16-byte rows, conflict-free ds_read_b128).  A wave encodes
+// sets of 64 tokens, block after block: the set's four groups of 16 tokens
+// are the columns of four MFMA products per codebook tile, which share the
+// tile's one LDS read, and the key blocks of the next block are in flight
+// meanwhile.  Each lane keeps, per
+// group, the running minimum of its 64 distances as the distance bits with
+// the low 8 bits replaced by the centroid's position in the lane (tile, row),
+// so one v_min3_u32 tracks value and index of two distances (distances are
+// positive: delta is added to every one) and a v_med3_u32 / v_min_u32 pair the
+// runner-up.  The four k-group lanes of every token are then merged by
+// v_permlane32_swap / v_permlane16_swap reduce-scatters (the k-group goes into
+// tag bits 7:6), leaving token l of the set in lane l for the clear test, the
+// index, the store and the exact recount.
 #include "encode_internal.h"
 
 namespace smaq {
@@ -84,28 +91,36 @@ __device__ __forceinline__ uint32_t min3_u32(uint32_t a, uint32_t b, uint32_t c)
   return r;
 }
 
-// The lanes l ^ 16 (X16) and l ^ 32 (X32) as VALU permutes: with both
-// operands x, v_permlane16_swap / v_permlane32_swap leave each lane the pair
-// {x[l], x[l ^ 16]} / {x[l], x[l ^ 32]} (in some order), which is all a
-// symmetric reduction (min, sum) needs -- no LDS round trip.
-struct LanePair {
-  uint32_t a, b;
-};
-__device__ __forceinline__ LanePair pair_x16(uint32_t x) {
-  const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
-  return {r[0], r[1]};
+// Cross-row exchanges without LDS.  A set of 64 tokens in MFMA layout: value
+// v[g] of lane (row r, column n) belongs to token (g, n), k-group r.  With
+// operands x, y,
+// v_permlane32_swap leaves {x rows 0-1 | y rows 0-1} and {x rows 2-3 | y
+// rows 2-3}, and v_permlane16_swap {x r0, y r0, x r2, y r2} and {x r1, y r1,
+// x r3, y r3}: swapping groups (0, 2) and (1, 3) across the halves, then the
+// two results across row pairs, hands lane (r, n) the four k-group values of
+// token (r, n).
+//
+// Sum over the four k-groups of token (r, n), delivered to lane (r, n):
+// (v[kg 0] + v[kg 2]) + (v[kg 1] + v[kg 3]).
+__device__ __forceinline__ float reduce_scatter_kgroups(const float* v) {
+  const auto p = __builtin_amdgcn_permlane32_swap(fbits(v[0]), fbits(v[2]), false, false);
+  const auto q = __builtin_amdgcn_permlane32_swap(fbits(v[1]), fbits(v[3]), false, false);
+  const float s02 = bitsf(p[0]) + bitsf(p[1]);  // rows 0-1: token (0, n), rows 2-3: (2, n)
+  const float s13 = bitsf(q[0]) + bitsf(q[1]);  // rows 0-1: token (1, n), rows 2-3: (3, n)
+  const auto r = __builtin_amdgcn_permlane16_swap(fbits(s02), fbits(s13), false, false);
+  return bitsf(r[0]) + bitsf(r[1]);
 }
-__device__ __forceinline__ LanePair pair_x32(uint32_t x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
-  return {r[0], r[1]};
-}
-// (x[l] + x[l ^ 16]) + (x[l ^ 32] + x[l ^ 48]): the same value, bit for bit,
-// in all four lanes of a token (fp32 addition commutes)
-__device__ __forceinline__ float sum_kgroups(float x) {
-  const LanePair p = pair_x16(fbits(x));
-  const float s = bitsf(p.a) + bitsf(p.b);
-  const LanePair q = pair_x32(fbits(s));
-  return bitsf(q.a) + bitsf(q.b);
+// The inverse direction: x of lane (r, n) belongs to token (r, n); every lane
+// of column n receives out[g] = x of token (g, n).
+__device__ __forceinline__ void all_gather_kgroups(float x, float* out) {
+  const auto a = __builtin_amdgcn_permlane16_swap(fbits(x), fbits(x), false, false);
+  // a[0]: token (0, n) on rows 0-1, (2, n) on rows 2-3; a[1]: (1, n) / (3, n)
+  const auto c0 = __builtin_amdgcn_permlane32_swap(a[0], a[0], false, false);
+  const auto c1 = __builtin_amdgcn_permlane32_swap(a[1], a[1], false, false);
+  out[0] = bitsf(c0[0]);
+  out[1] = bitsf(c1[0]);
+  out[2] = bitsf(c0[1]);
+  out[3] = bitsf(c1[1]);
 }
 
 // Orders this wave's LDS writes before its later LDS reads of other lanes'
@@ -283,128 +298,179 @@ __global__ __launch_bounds__(kVmThreads) void encode_blockvq_mfma_kernel(
   const uint32_t a_src = kg < 2 ? (uint32_t)(L.ch() + n * 16) : (kg == 2 ? (uint32_t)(L.cl() + n * 16) : (uint32_t)(L.cq() + n * 16));
   const uint32_t a_blk = kg < 3 ? (uint32_t)(kVmNc * 16) : 0u;  // A bytes per block (q rows: per 4 blocks)
   unsigned ties = 0;
-  const int64_t n_tiles = (rows + 15) / 16;
+  // A wave encodes sets of 64 tokens.  Group g (0..3) of a set is its tokens
+  // 16g + n, one MFMA column n each; the four groups share every codebook
+  // tile (one A read feeds four products).  The k-group partial results are
+  // then reduce-scattered so that lane l holds token l of the set, and the
+  // per-token tail (clear test, index, store, exact recount) runs once per
+  // token instead of once per k-group lane.
+  const int64_t n_sets = (rows + 63) / 64;
   const int64_t stride = (int64_t)gridDim.x * kVmWaves;
-  int64_t tile = (int64_t)blockIdx.x * kVmWaves + w;
-  auto key_row = [&](int64_t t) -> const T* {
-    const int64_t row = t * 16 + n;
+  int64_t set = (int64_t)blockIdx.x * kVmWaves + w;
+  auto key_row = [&](int64_t s, int g) -> const T* {
+    const int64_t row = s * 64 + 16 * g + n;
     return k + map.offset(row < rows ? row : rows - 1);
   };
-  // (key_row clamps past-the-end rows, so the prefetch past the last tile
+  // (key_row clamps past-the-end rows, so the prefetch past the last set
   // reads a valid row)
-  const T* kr = key_row(tile);
-  KeyBlock<T> next;
-  next.load(kr);
-  for (; tile < n_tiles; tile += stride) {
-    const int64_t row = tile * 16 + n;
+  const T* kp[4];
+  KeyBlock<T> kb[4];  // this group's token: the key block in flight
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    kp[g] = key_row(set, g);
+    kb[g].load(kp[g]);
+  }
+  const uint32_t kg_tag = (uint32_t)kg << 6;
+  for (; set < n_sets; set += stride) {
+    const int64_t row = set * 64 + lane;  // the token this lane finishes
     const bool valid = row < rows;
     uint8_t* const out = idx_out + map.out_row(valid ? row : 0) * nb;
-    const T* const kr_next = key_row(tile + stride);
     for (int b = 0; b < nb; ++b) {
-      float kv[kVmBd];
-      next.unpack(kv);
-      // the next key block of this lane's token (or the next tile's first)
-      next.load(b + 1 < nb ? kr + (b + 1) * kVmBd : kr_next);
       // rows kg and kg + 4 of E_b, 16-byte reads
       const LdsF32x4* er = (const LdsF32x4*)(lds3 + L.es() + (size_t)b * 256 + kg * 32);
       const f32x4 ea0 = er[0], ea1 = er[1], eb0 = er[8], eb1 = er[9];  // row kg + 4: 128 bytes on
       const float ea[kVmBd] = {ea0[0], ea0[1], ea0[2], ea0[3], ea1[0], ea1[1], ea1[2], ea1[3]};
       const float eb[kVmBd] = {eb0[0], eb0[1], eb0[2], eb0[3], eb1[0], eb1[1], eb1[2], eb1[3]};
-      // x_kg and x_{kg+4}: the reference's chain, bit for bit
-      float xa = 0.0f, xb = 0.0f;
-#pragma unroll
-      for (int d = 0; d < kVmBd; ++d) {
-        xa = fmaf(kv[d], ea[d], xa);
-        xb = fmaf(kv[d], eb[d], xb);
-      }
       const float sg = sig_all[b];
-      const float ya = xa * (-2.0f * sg), yb = xb * (-2.0f * sg);  // exact (powers of two)
-      const bool ok = fabsf(ya) < kYMax && fabsf(yb) < kYMax;     // false for NaN
-      const _Float16 yah = (_Float16)ya, ybh = (_Float16)yb;
-      const _Float16 yal = (_Float16)(ya - (float)yah), ybl = (_Float16)(yb - (float)ybh);
-      *(__attribute__((address_space(3))) uint32_t*)(lds3 + ys_tok + 4 * kg) = h16(yah) | (h16(ybh) << 16);
-      *(__attribute__((address_space(3))) uint32_t*)(lds3 + ys_tok + 16 + 4 * kg) = h16(yal) | (h16(ybl) << 16);
-      float sq = ok ? xa * xa + xb * xb : __builtin_nanf("");
-      sq = sum_kgroups(sq);
-      const float delta = kDeltaRel * (sq + smax_all[b]);
-      const float s2 = sg * sg;
-      const float init = (sq + delta) * s2;  // |x|^2 + delta, scaled
+      const float m2s = -2.0f * sg, s2 = sg * sg, smax_b = smax_all[b];
+      // ---- the four groups' B operands (staged one group at a time through
+      // the wave's 16-token buffer) and C operands sigma^2 (|x|^2 + delta)
+      f16x8 bv[4];
+      float sqp[4];  // this k-group's part of |x|^2 of token (g, n)
+      // the key blocks loaded next: block b + 1 of these tokens, or block 0
+      // of the next set's
+      const bool last = b + 1 == nb;
+      if (last) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) kp[g] = key_row(set + stride, g);
+      }
+      const int next_off = last ? 0 : (b + 1) * kVmBd;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        float kv[kVmBd];
+        kb[g].unpack(kv);
+        kb[g].load(kp[g] + next_off);
+        // x_kg and x_{kg+4}: the reference's chain, bit for bit
+        float xa = 0.0f, xb = 0.0f;
+#pragma unroll
+        for (int d = 0; d < kVmBd; ++d) {
+          xa = fmaf(kv[d], ea[d], xa);
+          xb = fmaf(kv[d], eb[d], xb);
+        }
+        const float ya = xa * m2s, yb = xb * m2s;                 // exact (powers of two)
+        const bool ok = fabsf(ya) < kYMax && fabsf(yb) < kYMax;  // false for NaN
+        const _Float16 yah = (_Float16)ya, ybh = (_Float16)yb;
+        const _Float16 yal = (_Float16)(ya - (float)yah), ybl = (_Float16)(yb - (float)ybh);
+        *(__attribute__((address_space(3))) uint32_t*)(lds3 + ys_tok + 4 * kg) = h16(yah) | (h16(ybh) << 16);
+        *(__attribute__((address_space(3))) uint32_t*)(lds3 + ys_tok + 16 + 4 * kg) = h16(yal) | (h16(ybl) << 16);
+        sqp[g] = ok ? xa * xa + xb * xb : __builtin_nanf("");
+        wave_sync();
+        // B: k-group 0 / 2 take y hi, 1 takes y lo, 3 the 2^14 pair of block b
+        bv[g] = __builtin_bit_cast(f16x8, *(LdsU32x4*)(lds3 + b_src + (kg == 3 ? (uint32_t)(b & 3) * 16u : 0u)));
+        // the next group's staging stores come after this read: a wave's LDS
+        // operations execute in order, so only the compiler must keep them so
+        asm volatile("" ::: "memory");
+      }
+      // ---- |x|^2 of token (kg, n) in this lane (the four k-group parts
+      // reduce-scattered), delta and the accumulator start sigma^2 (|x|^2 +
+      // delta) once per token, then the four groups' starts gathered back
+      const float sq = reduce_scatter_kgroups(sqp);
+      const float delta = kDeltaRel * (sq + smax_b);
       const float delta_s = delta * s2;
-      wave_sync();
-      // B: k-group 0 / 2 take y hi, 1 takes y lo, 3 the 2^14 pair of block b
-      const f16x8 bv = __builtin_bit_cast(
-          f16x8, *(LdsU32x4*)(lds3 + b_src + (kg == 3 ? (uint32_t)(b & 3) * 16u : 0u)));
+      float init_g[4];
+      all_gather_kgroups((sq + delta) * s2, init_g);
+      f32x4 cv[4];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) cv[g] = f32x4{init_g[g], init_g[g], init_g[g], init_g[g]};
+      // ---- distances: tile t of 16 centroids for each group, the product of
+      // the next (tile, group) issued before the keys of this one are reduced
       const LdsU32x4* ap =
           (LdsU32x4*)(lds3 + a_src + (kg < 3 ? (uint32_t)b * a_blk : (uint32_t)(b >> 2) * (uint32_t)(kVmNc * 16)));
-      const f32x4 acc0 = {init, init, init, init};
-      uint32_t best = 0xffffffffu, second = 0xffffffffu;
-      // software pipelined: the product of tile t + 1 is issued before the
-      // keys of tile t are reduced, and the A operand of tile t + 3 is read
-      // then (two tiles of LDS latency covered)
-      u32x4 a_n1 = ap[16], a_n2 = ap[32];
-      f32x4 acc_next = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, ap[0]), bv, acc0, 0, 0, 0);
+      uint32_t best[4], second[4];
 #pragma unroll
-      for (int t = 0; t < 16; ++t) {
+      for (int g = 0; g < 4; ++g) best[g] = second[g] = 0xffffffffu;
+      u32x4 a_cur = ap[0], a_nxt = ap[16];
+      f32x4 acc_next = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a_cur), bv[0], cv[0], 0, 0, 0);
+#pragma unroll
+      for (int s = 0; s < 64; ++s) {
+        const int t = s >> 2, g = s & 3;
         const f32x4 acc = acc_next;
-        if (t + 1 < 16) {
-          acc_next = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a_n1), bv, acc0, 0, 0, 0);
-          a_n1 = a_n2;
-          if (t + 3 < 16) a_n2 = ap[16 * (t + 3)];
+        if (s + 1 < 64) {
+          const int t1 = (s + 1) >> 2, g1 = (s + 1) & 3;
+          if (g1 == 0) {
+            a_cur = a_nxt;
+            if (t1 + 1 < 16) a_nxt = ap[16 * (t1 + 1)];
+          }
+          acc_next = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a_cur), bv[g1], cv[g1], 0, 0, 0);
         }
 #pragma unroll
         for (int i = 0; i < 4; i += 2) {
-          // centroids 16t + 4kg + i, i + 1 of token n; low 6 bits = (t, i)
-          const uint32_t k0 = (fbits(acc[i]) & 0xffffffc0u) | (uint32_t)(4 * t + i);
-          const uint32_t k1 = (fbits(acc[i + 1]) & 0xffffffc0u) | (uint32_t)(4 * t + i + 1);
-          second = min(second, med3_u32(best, k0, k1));
-          best = min3_u32(best, k0, k1);
+          // centroids 16t + 4kg + i, i + 1 of token (g, n); low 8 bits =
+          // (0, t, i) now, the k-group goes into bits 6-7 below
+          const uint32_t k0 = (fbits(acc[i]) & 0xffffff00u) | (uint32_t)(4 * t + i);
+          const uint32_t k1 = (fbits(acc[i + 1]) & 0xffffff00u) | (uint32_t)(4 * t + i + 1);
+          second[g] = min(second[g], med3_u32(best[g], k0, k1));
+          best[g] = min3_u32(best[g], k0, k1);
         }
       }
-      // merge the four k-group lanes of each token
-      uint32_t gbest = best, gsecond = second;
+      // ---- merge the four k-group lanes of every token, leaving token
+      // 16r + n (group r, column n) in lane 16r + n: lanes l ^ 32 for the
+      // group pairs (0, 2), (1, 3), then lanes l ^ 16.  With best <= second
+      // on both sides, the merged runner-up is min(second_a, second_b,
+      // max(best_a, best_b)).
 #pragma unroll
-      for (int step = 0; step < 2; ++step) {  // lanes l ^ 16, then l ^ 32
-        const LanePair pb = step == 0 ? pair_x16(gbest) : pair_x32(gbest);
-        const LanePair ps = step == 0 ? pair_x16(gsecond) : pair_x32(gsecond);
-        gsecond = min3_u32(ps.a, ps.b, max(pb.a, pb.b));
-        gbest = min(pb.a, pb.b);
+      for (int g = 0; g < 4; ++g) best[g] |= kg_tag;
+      uint32_t mb[2], ms[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const auto pb = __builtin_amdgcn_permlane32_swap(best[h], best[h + 2], false, false);
+        const auto ps = __builtin_amdgcn_permlane32_swap(second[h], second[h + 2], false, false);
+        mb[h] = min(pb[0], pb[1]);
+        ms[h] = min3_u32(ps[0], ps[1], max(pb[0], pb[1]));
       }
-      const float vb = bitsf(gbest & 0xffffffc0u), vs = bitsf(gsecond & 0xffffffc0u);
+      const auto pb = __builtin_amdgcn_permlane16_swap(mb[0], mb[1], false, false);
+      const auto ps = __builtin_amdgcn_permlane16_swap(ms[0], ms[1], false, false);
+      const uint32_t gbest = min(pb[0], pb[1]);
+      const uint32_t gsecond = min3_u32(ps[0], ps[1], max(pb[0], pb[1]));
+      const float vb = bitsf(gbest & 0xffffff00u), vs = bitsf(gsecond & 0xffffff00u);
       // clear winner: the runner-up more than delta behind (keys are
-      // truncated by at most 2^-17 relative); distances positive and finite
-      const bool clear = (vs - vb * (1.0f + 0x1p-16f) > delta_s) && vb > 0.0f && vb < 3.0e38f &&
+      // truncated by less than 2^-15 relative); distances positive and finite
+      const bool clear = (vs - vb * (1.0f + 0x1p-14f) > delta_s) && vb > 0.0f && vb < 3.0e38f &&
                          delta_s < 3.0e38f;
-      const int kw = best == gbest ? kg : 4;  // the lane holding the winner
-      int kwin = kw;
-      {
-        const LanePair p = pair_x16((uint32_t)kwin);
-        const LanePair q = pair_x32(min(p.a, p.b));
-        kwin = (int)min(q.a, q.b);
-      }
-      const int tag = (int)(gbest & 63u);
-      int idx = 16 * (tag >> 2) + 4 * kwin + (tag & 3);
+      // tag bits: kg (7:6), t (5:2), i (1:0) -> centroid 16t + 4kg + i
+      const uint32_t tag = gbest & 0xffu;
+      int idx = (int)(((tag & 0x3cu) << 2) | ((tag >> 4) & 0xcu) | (tag & 3u));
       // exact recount of the unclear tokens, one at a time by the whole wave
-      uint64_t todo = __ballot(!clear && valid && kg == 0);
+      uint64_t todo = __ballot(!clear && valid);
       while (todo) {
         const int t0 = __builtin_ctzll(todo);
         todo &= todo - 1;
-        float x[kVmBd];
+        // x of token t0 again (the same chain), from its key block
+        const int64_t r0 = set * 64 + t0;
+        KeyBlock<T> kx;
+        kx.load(k + map.offset(r0) + b * kVmBd);
+        float kv[kVmBd], x[kVmBd];
+        kx.unpack(kv);
+        const float* Eb = E_blocks + b * 64;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          x[e] = __shfl(xa, t0 + 16 * e, 64);
-          x[e + 4] = __shfl(xb, t0 + 16 * e, 64);
+        for (int e = 0; e < kVmBd; ++e) {
+          float a = 0.0f;
+#pragma unroll
+          for (int d = 0; d < kVmBd; ++d) a = fmaf(kv[d], Eb[e * kVmBd + d], a);
+          x[e] = a;
         }
         float xsq = 0.0f;
 #pragma unroll
         for (int e = 0; e < kVmBd; ++e) xsq = xsq + x[e] * x[e];  // x.pow(2).sum(-1) order
         bool tie;
         const int ci = exact_argmin(x, xsq, C + (int64_t)b * kVmNc * kVmBd, lane, &tie);
-        if (n == t0) idx = ci;
-        if (lane == t0) ties += tie ? 1u : 0u;
+        if (lane == t0) {
+          idx = ci;
+          ties += tie ? 1u : 0u;
+        }
       }
-      if (valid && kg == 0) out[b] = (uint8_t)idx;
+      if (valid) out[b] = (uint8_t)idx;
     }
-    kr = kr_next;
   }
   add_count(tie_count, ties);
 }

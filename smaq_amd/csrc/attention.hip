@@ -448,8 +448,8 @@ extern "C" long long smaq_attn_workspace_bytes(const smaq_attn_params* p) {
   int64_t bytes = partial_bytes(p, pl);
   if (pl.longest_first) bytes = align256(bytes) + (int64_t)p->batch * (int64_t)sizeof(int);
   if (pl.prefill) {
-    // four f16 planes (key hi/lo, value hi/lo) per part
-    const int64_t per_tok = (int64_t)p->batch * p->n_kv_heads * p->head_dim * 4 * 2;
+    // kPrefillPlanes f16 planes (key hi, key lo, values) per part
+    const int64_t per_tok = (int64_t)p->batch * p->n_kv_heads * p->head_dim * kPrefillPlanes * 2;
     bytes = align256(bytes) + align256(pl.hist_lp * per_tok) + align256(pl.recent_lp * per_tok);
   }
   return bytes;
@@ -538,7 +538,7 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
       PrefillPlanes P;
       P.img = (_Float16*)ws;
       P.Lp = lp;
-      ws += align256(n_el * 4 * 2);
+      ws += align256(n_el * kPrefillPlanes * 2);
       return P;
     };
     const PrefillPlanes hp = planes(pl.hist_lp);

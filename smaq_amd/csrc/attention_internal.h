@@ -33,9 +33,11 @@ struct Partials {
 
 
 // Matrix-core prefill path (attention_prefill.hip).  Each attended part
-// (history, recent window) is first decoded into f16 hi/lo tile images:
-// [B][Hkv][Lp / 64] tiles of 64 KB, each the LDS image the kernel copies
-// (key hi, key lo, value hi, value lo; layout in attention_prefill.hip).
+// (history, recent window) is first decoded into f16 tile images:
+// [B][Hkv][Lp / 64] tiles of 48 KB, each the LDS image the kernel copies
+// (key hi, key lo, values: kPrefillPlanes f16 planes of head_dim x 64;
+// layout in attention_prefill.hip).
+constexpr int kPrefillPlanes = 3;
 struct PrefillPlanes {
   _Float16* img;
   int64_t Lp;  // padded tokens per (sequence, KV head), multiple of 64

@@ -1,19 +1,23 @@
 // Chunked-prefill attention on the gfx950 matrix cores (head_dim 128).
 //
 // Prefill is compute-bound (every key tile serves many query rows), so the
-// packed cache is first decoded once per part into f16 hi/lo tile images in
-// the workspace (the dequantisation the generic kernels do per query tile):
+// packed cache is first decoded once per part into f16 tile images in the
+// workspace (the dequantisation the generic kernels do per query tile):
 //   keys   K~[t][d]  = lut[code] * norm (scalar) or decoded centroid (block-VQ);
-//                      the recent window's exact keys
+//                      the recent window's exact keys; hi = f16(x) and
+//                      lo = f16(x - hi), ~22 significant bits
 //   values V^[d][t]  = code * scale + zero (fp32, as the reference's
-//                      dequantize_values), stored dimension-major
-// each as hi = f16(x), lo = f16(x - hi), ~22 significant bits.
+//                      dequantize_values), stored dimension-major as f16(x)
+// The values' rounding moves an output by at most 2^-12 max|v| (+2^-25):
+// o = sum p v / sum p with every v off by at most 2^-12 |v| -- 6e-4 for
+// values within +-2.5, inside the 2e-3 max-abs / 1e-3 relative budget; the
+// recent window's fp16 / bf16 values are exact in f16.
 //
-// Tile image (64 tokens of one (sequence, KV head), 64 KB, exactly what the
+// Tile image (64 tokens of one (sequence, KV head), 48 KB, exactly what the
 // kernel holds in LDS):
 //   [K hi | K lo]  64 key rows x 256 B; 16-byte unit u (dims 8u..8u+7) of
 //                  row r sits at unit u ^ (r & 15)
-//   [V hi | V lo]  128 dim rows x 128 B; unit u = 4 st + kg holds keys
+//   [V]            128 dim rows x 128 B; unit u = 4 st + kg holds keys
 //                  32 st + 4 kg + {0..3} and 32 st + 16 + 4 kg + {0..3} (the
 //                  eight k-elements one lane feeds the PV matrix op), at unit
 //                  u ^ ((d >> 1) & 7) of row d
@@ -28,7 +32,7 @@
 //   softmax per query column (keys = C rows: 4 per lane, 4 lane groups)
 //   O^T[dim][query] += V^T . P^T  A = value rows (dimension-major tile),
 //                                B = P^T straight from the S^T accumulators
-// with qh.kh + qh.kl + ql.kh and vh.ph + vh.pl + vl.ph.  Each workgroup (8
+// with qh.kh + qh.kl + ql.kh and v.ph + v.pl.  Each workgroup (8
 // waves x 32 query rows) streams the 64-key tiles of one (sequence, query
 // head, key split), double-buffered: the next tile is copied straight into
 // LDS (global_load_lds_dwordx4) while the current one is computed.  It writes
@@ -54,8 +58,8 @@ constexpr int kQW = 32;           // query rows per wave
 constexpr int kPW = 8;            // waves per workgroup
 constexpr int kPT = 64 * kPW;     // threads per workgroup
 constexpr int kQB = kPW * kQW;    // query rows per workgroup
-constexpr int kImg = 32768;       // halves per tile image (64 KB)
-constexpr int kImgKL = 8192, kImgVH = 16384, kImgVL = 24576;  // part offsets (halves)
+constexpr int kImg = 8192 * kPrefillPlanes;  // halves per tile image (48 KB)
+constexpr int kImgKL = 8192, kImgV = 16384;   // part offsets (halves)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazy = 8.0f;     // softmax reference max raised by > 2^8 only
 
@@ -111,12 +115,10 @@ __device__ __forceinline__ void store_values(_Float16* img, const float (*vs)[kK
 #pragma unroll
   for (int kg = 0; kg < 4; ++kg) {
     const int u = 4 * st + kg;
-    _Float16 hi[8], lo[8];
+    _Float16 v[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) split_f16(vs[d][vunit_key(u, e)], hi[e], lo[e]);
-    const int off = vimg_off(d, u);
-    *(uint4*)(img + kImgVH + off) = pack8(hi);
-    *(uint4*)(img + kImgVL + off) = pack8(lo);
+    for (int e = 0; e < 8; ++e) v[e] = (_Float16)vs[d][vunit_key(u, e)];
+    *(uint4*)(img + kImgV + vimg_off(d, u)) = pack8(v);
   }
 }
 
@@ -359,7 +361,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     __syncthreads();
     if (kt0 + kKT < k1) copy_tile(kt0 + kKT, (it + 1) & 1);
     const _Float16* kimg = tiles[it & 1];
-    const _Float16* vimg = tiles[it & 1] + kImgVH;
+    const _Float16* vimg = tiles[it & 1] + kImgV;
     // ---- S^T = K Q^T: keys 16kb + 4kg + v (rows), query 16qb + n (column)
     f32x4 sacc[2][4];
 #pragma unroll
@@ -452,16 +454,13 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         // A: dim 16db + n, keys 32st + 4kg + 0..3 and 32st + 16 + 4kg + 0..3
         // (one unit of the value image)
         const int off = vimg_off(16 * db + n, 4 * st + kg);
-        const u32x4 avh = *(const u32x4*)&vimg[off];
-        const u32x4 avl = *(const u32x4*)&vimg[kImgVL - kImgVH + off];
+        const u32x4 av = *(const u32x4*)&vimg[off];
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) {
-          acc_o[qb][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, avh),
+          acc_o[qb][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av),
                                                                  __builtin_bit_cast(f16x8, ph[qb][st]), acc_o[qb][db], 0, 0, 0);
-          acc_o[qb][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, avh),
+          acc_o[qb][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av),
                                                                  __builtin_bit_cast(f16x8, pl[qb][st]), acc_o[qb][db], 0, 0, 0);
-          acc_o[qb][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, avl),
-                                                                 __builtin_bit_cast(f16x8, ph[qb][st]), acc_o[qb][db], 0, 0, 0);
         }
       }
     __builtin_amdgcn_s_setprio(0);
@@ -502,7 +501,7 @@ bool prefill_mfma_supported(const smaq_attn_params& p) {
 
 int64_t prefill_padded_len(int64_t L) { return ((L + kKT - 1) / kKT) * kKT; }
 
-// Workgroups hold 128 KB of LDS, one per CU.  Split the keys so that the
+// Workgroups hold 96 KB of LDS, one per CU.  Split the keys so that the
 // grid covers at least three rounds of the device's CUs and, among up to
 // twice that many splits, the one whose last round is fullest (splits of at
 // least four tiles).

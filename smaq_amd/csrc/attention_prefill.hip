@@ -61,6 +61,10 @@ constexpr int kQB = kPW * kQW;    // query rows per workgroup
 constexpr int kImg = 8192 * kPrefillPlanes;  // halves per tile image (48 KB)
 constexpr int kImgKL = 8192, kImgV = 16384;   // part offsets (halves)
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kCopyLoads = kImg * 2 / 16 / kPT;  // 16-byte direct-to-LDS loads per thread and tile
+// s_waitcnt immediate: vmcnt <= kCopyLoads, expcnt and lgkmcnt not waited
+constexpr int kWaitTileAhead = (15 << 8) | (7 << 4) | kCopyLoads;
+static_assert(kCopyLoads == 6 && kImg * 2 == kCopyLoads * 16 * kPT, "tile copy: whole 16-byte loads per thread");
 constexpr float kLazy = 8.0f;     // softmax reference max raised by > 2^8 only
 
 // halves offset of 16-byte unit u of key row r / value row d in a tile image part
@@ -74,6 +78,21 @@ __device__ __forceinline__ uint32_t h16(_Float16 h) { return (uint32_t)__builtin
 __device__ __forceinline__ void split_f16(float x, _Float16& hi, _Float16& lo) {
   hi = (_Float16)x;
   lo = (_Float16)(x - (float)hi);
+}
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// split_f16 of two numbers, packed: hi = RN(x) of both in one packed
+// convert; x - hi (exact in fp32) by two mixed-precision FMAs x * one - hi
+// reading hi as f16, and the lo pair in one more packed convert.  `one` is
+// 1.0 kept opaque to the compiler, so that the FMA is not folded into an
+// add (which has no mixed-precision form).
+__device__ __forceinline__ void split2_f16(float x0, float x1, float one, uint32_t& hi, uint32_t& lo) {
+  const f16x2 h = __builtin_convertvector((f32x2){x0, x1}, f16x2);
+  const f32x2 r = {__builtin_fmaf(one, x0, -(float)h[0]), __builtin_fmaf(one, x1, -(float)h[1])};
+  hi = __builtin_bit_cast(uint32_t, h);
+  lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, f16x2));
 }
 
 __device__ __forceinline__ int exponent_of(float x) {
@@ -247,7 +266,7 @@ __global__ __launch_bounds__(256) void decode_recent_planes_kernel(smaq_attn_par
 template <bool CAUSAL>
 __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_mfma_kernel(
     smaq_attn_params p, PrefillPart pp, Partials part) {
-  __shared__ __attribute__((aligned(16))) _Float16 tiles[2][kImg];   // double-buffered tile images
+  __shared__ __attribute__((aligned(16))) _Float16 tiles[3][kImg];   // ring of three tile images
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int n = lane & 15, kg = lane >> 4;
@@ -343,25 +362,42 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // load j of wave w covers units 512 j + 64 w .. + 63, contiguous in LDS
   const _Float16* img0 = pp.img + ((int64_t)b * p.n_kv_heads + h) * (pp.Lp / kKT) * kImg;
   const int wu = __builtin_amdgcn_readfirstlane(w);
+  // (unit 512 j + tid sits 16 (512 j + tid) bytes into the image: a
+  // wave-uniform base plus one 32-bit lane offset, the loads' SGPR-base form)
+  const uint32_t lane_off = 16u * (uint32_t)tid;
   auto copy_tile = [&](int64_t kt, int buf) {
-    const _Float16* src = img0 + (kt / kKT) * kImg;
+    const char* src = (const char*)(img0 + (kt / kKT) * kImg);
 #pragma unroll
-    for (int j = 0; j < kImg * 2 / 16 / kPT; ++j) {
+    for (int j = 0; j < kCopyLoads; ++j) {
       const int unit0 = kPT * j + 64 * wu;
-      __builtin_amdgcn_global_load_lds((const void*)(src + 8 * (unit0 + lane)),
+      __builtin_amdgcn_global_load_lds((const void*)(src + 16 * kPT * j + lane_off),
                                        (__attribute__((address_space(3))) void*)(&tiles[buf][8 * unit0]), 16, 0, 0);
     }
   };
+  // tiles i + 1 and i + 2 are in flight while tile i is computed
   if (k0 < k1) copy_tile(k0, 0);
-  int it = 0;
-  for (int64_t kt0 = k0; kt0 < k1; kt0 += kKT, ++it) {
-    // this tile's copy has landed for every thread, and every wave is done
-    // with the other buffer, which then takes the next tile
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (kt0 + kKT < k1) copy_tile(kt0 + kKT, (it + 1) & 1);
-    const _Float16* kimg = tiles[it & 1];
-    const _Float16* vimg = tiles[it & 1] + kImgV;
+  if (k0 + kKT < k1) copy_tile(k0 + kKT, 1);
+  float one = 1.0f;  // opaque to the compiler (see split2_f16)
+  asm volatile("" : "+v"(one));
+  int buf = 0;  // ring buffer of tile i
+  for (int64_t kt0 = k0; kt0 < k1; kt0 += kKT) {
+    // this thread's copies of tile i have landed (copies complete in order;
+    // only tile i + 1's kCopyLoads may still be in flight), then every
+    // thread's have, and every wave is done with tile i - 1, whose buffer
+    // takes tile i + 2.  The barrier carries no memory fence (which would
+    // wait for tile i + 1 too); the empty asm statements keep the compiler
+    // from moving LDS accesses across it.
+    if (kt0 + kKT < k1)
+      __builtin_amdgcn_s_waitcnt(kWaitTileAhead);
+    else
+      __builtin_amdgcn_s_waitcnt(0);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (kt0 + 2 * kKT < k1) copy_tile(kt0 + 2 * kKT, buf == 0 ? 2 : buf - 1);
+    const _Float16* kimg = tiles[buf];
+    const _Float16* vimg = tiles[buf] + kImgV;
+    buf = buf == 2 ? 0 : buf + 1;
     // ---- S^T = K Q^T: keys 16kb + 4kg + v (rows), query 16qb + n (column)
     f32x4 sacc[2][4];
 #pragma unroll
@@ -392,23 +428,34 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
       }
     __builtin_amdgcn_s_setprio(0);
-    // ---- softmax per query column (base 2, lazily raised reference max)
+    // ---- softmax per query column (base 2, lazily raised reference max).
+    // When every column of the wave sees all 64 keys of the tile (no causal
+    // or length cut), the maximum is taken on the raw scores (qfac > 0
+    // commutes with it) and a weight is exp2(s qfac - m), one fused
+    // multiply-add; boundary tiles and columns with no visible key yet take
+    // the masked form.
     u32x4 ph[2][2], pl[2][2];  // [qb][32-key step]: P^T as B operands
+    const bool plain = __all(kt0 + kKT <= vis[0] && kt0 + kKT <= vis[1]);
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
       // keys kt0 + i are visible to this column for i < lim
       const int lim = (int)max((int64_t)-1, min((int64_t)kKT, vis[qb] - kt0));
-      float sv[16];
       float mt = -__builtin_inff();
+      if (plain) {
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
+        for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          float x = sacc[qb][kb][v] * qfac[qb];
-          if (16 * kb + 4 * kg + v >= lim) x = -__builtin_inff();
-          sv[4 * kb + v] = x;
-          mt = fmaxf(mt, x);
-        }
+          for (int v = 0; v < 4; ++v) mt = fmaxf(mt, sacc[qb][kb][v]);
+        mt *= qfac[qb];
+      } else {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const float x = sacc[qb][kb][v] * qfac[qb];
+            mt = fmaxf(mt, 16 * kb + 4 * kg + v >= lim ? -__builtin_inff() : x);
+          }
+      }
       mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
       mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
       if (__any(mt > m_thr[qb])) {
@@ -423,21 +470,34 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const bool dead = m_run[qb] == -__builtin_inff();
       float ls = 0.0f;
       uint32_t hw[2][4], lw[2][4];
+      // step kb >> 1; elements 0..3 from the even key block, 4..7 the odd one
+      if (plain && !__any(dead)) {
+        const float mneg = -m_run[qb];
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
+        for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int v = 0; v < 4; v += 2) {
-          const float p0 = dead ? 0.0f : __builtin_amdgcn_exp2f(sv[4 * kb + v] - m_run[qb]);
-          const float p1 = dead ? 0.0f : __builtin_amdgcn_exp2f(sv[4 * kb + v + 1] - m_run[qb]);
-          ls += p0 + p1;
-          _Float16 h0, l0, h1, l1;
-          split_f16(p0, h0, l0);
-          split_f16(p1, h1, l1);
-          // step kb >> 1; elements 0..3 from the even key block, 4..7 the odd one
-          const int dw = 2 * (kb & 1) + (v >> 1);
-          hw[kb >> 1][dw] = h16(h0) | (h16(h1) << 16);
-          lw[kb >> 1][dw] = h16(l0) | (h16(l1) << 16);
-        }
+          for (int v = 0; v < 4; v += 2) {
+            const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[qb][kb][v], qfac[qb], mneg));
+            const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[qb][kb][v + 1], qfac[qb], mneg));
+            ls += p0 + p1;
+            const int dw = 2 * (kb & 1) + (v >> 1);
+            split2_f16(p0, p1, one, hw[kb >> 1][dw], lw[kb >> 1][dw]);
+          }
+      } else {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int v = 0; v < 4; v += 2) {
+            float x0 = sacc[qb][kb][v] * qfac[qb], x1 = sacc[qb][kb][v + 1] * qfac[qb];
+            if (16 * kb + 4 * kg + v >= lim) x0 = -__builtin_inff();
+            if (16 * kb + 4 * kg + v + 1 >= lim) x1 = -__builtin_inff();
+            const float p0 = dead ? 0.0f : __builtin_amdgcn_exp2f(x0 - m_run[qb]);
+            const float p1 = dead ? 0.0f : __builtin_amdgcn_exp2f(x1 - m_run[qb]);
+            ls += p0 + p1;
+            const int dw = 2 * (kb & 1) + (v >> 1);
+            split2_f16(p0, p1, one, hw[kb >> 1][dw], lw[kb >> 1][dw]);
+          }
+      }
       l_run[qb] += ls;
 #pragma unroll
       for (int st = 0; st < 2; ++st) {

@@ -408,25 +408,33 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // overlap one's softmax with the other's matrix work: 4.66 -> 4.49 ms at
     // c4; a fixed priority difference between the two was slower)
     __builtin_amdgcn_s_setprio(1);
+    // two straight-line versions (with / without the query-lo products),
+    // chosen once per tile, so that no branch splits the matrix section
+    auto qk = [&](auto with_lo) {
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+      for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        // key row 16 kb + n, dims 32 ks + 8 kg .. + 7 (unit 4 ks + kg)
-        const int off = kimg_off(16 * kb + n, 4 * ks + kg);
-        const u32x4 ah = *(const u32x4*)&kimg[off];
-        const u32x4 al = *(const u32x4*)&kimg[kImgKL + off];
+        for (int ks = 0; ks < 4; ++ks) {
+          // key row 16 kb + n, dims 32 ks + 8 kg .. + 7 (unit 4 ks + kg)
+          const int off = kimg_off(16 * kb + n, 4 * ks + kg);
+          const u32x4 ah = *(const u32x4*)&kimg[off];
+          const u32x4 al = *(const u32x4*)&kimg[kImgKL + off];
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-          sacc[qb][kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, ah),
-                                                                __builtin_bit_cast(f16x8, bqh[qb][ks]), sacc[qb][kb], 0, 0, 0);
-          sacc[qb][kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, al),
-                                                                __builtin_bit_cast(f16x8, bqh[qb][ks]), sacc[qb][kb], 0, 0, 0);
-          if (!q_lo_zero)
+          for (int qb = 0; qb < 2; ++qb) {
             sacc[qb][kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, ah),
-                                                                  __builtin_bit_cast(f16x8, bql[qb][ks]), sacc[qb][kb], 0, 0, 0);
+                                                                  __builtin_bit_cast(f16x8, bqh[qb][ks]), sacc[qb][kb], 0, 0, 0);
+            sacc[qb][kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, al),
+                                                                  __builtin_bit_cast(f16x8, bqh[qb][ks]), sacc[qb][kb], 0, 0, 0);
+            if constexpr (decltype(with_lo)::value)
+              sacc[qb][kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, ah),
+                                                                    __builtin_bit_cast(f16x8, bql[qb][ks]), sacc[qb][kb], 0, 0, 0);
+          }
         }
-      }
+    };
+    if (q_lo_zero)
+      qk(std::false_type{});
+    else
+      qk(std::true_type{});
     __builtin_amdgcn_s_setprio(0);
     // ---- softmax per query column (base 2, lazily raised reference max).
     // When every column of the wave sees all 64 keys of the tile (no causal

@@ -325,6 +325,10 @@ __global__ __launch_bounds__(kVmThreads) void encode_blockvq_mfma_kernel(
     const int64_t row = set * 64 + lane;  // the token this lane finishes
     const bool valid = row < rows;
     uint8_t* const out = idx_out + map.out_row(valid ? row : 0) * nb;
+    // the token's indices, byte b in word b / 4, stored together after the
+    // last block (one store per block and token leaves 16 partial writes of
+    // a row to reach HBM separately once the set's rows fall out of L2)
+    uint32_t ob[kVmMaxBlocks / 4] = {0u, 0u, 0u, 0u};
     for (int b = 0; b < nb; ++b) {
       // rows kg and kg + 4 of E_b, 16-byte reads
       const LdsF32x4* er = (const LdsF32x4*)(lds3 + L.es() + (size_t)b * 256 + kg * 32);
@@ -469,7 +473,20 @@ __global__ __launch_bounds__(kVmThreads) void encode_blockvq_mfma_kernel(
           ties += tie ? 1u : 0u;
         }
       }
-      if (valid) out[b] = (uint8_t)idx;
+      const uint32_t v = (uint32_t)idx << (8 * (b & 3));
+      switch (b >> 2) {  // b is wave-uniform: scalar branches
+        case 0: ob[0] |= v; break;
+        case 1: ob[1] |= v; break;
+        case 2: ob[2] |= v; break;
+        default: ob[3] |= v; break;
+      }
+    }
+    if (valid) {
+      if (nb == kVmMaxBlocks && ((uintptr_t)out & 15) == 0) {
+        *(u32x4*)out = u32x4{ob[0], ob[1], ob[2], ob[3]};
+      } else {
+        for (int b = 0; b < nb; ++b) out[b] = (uint8_t)(ob[b >> 2] >> (8 * (b & 3)));
+      }
     }
   }
   add_count(tie_count, ties);

@@ -34,6 +34,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import statistics
 import sys
 import time
@@ -52,7 +53,8 @@ F16_PEAK_TFLOPS = 2500.0
 # products of hi/lo splits (~22-bit scores), PV as two bf16 products of a
 # hi/lo split weight against exact 2-bit codes, fp32 softmax and accumulation.
 DECODE_DTYPE = "bf16 storage; QK 3x f16 hi/lo MFMA (~22-bit), PV 2x bf16 hi/lo MFMA on exact codes, fp32 accumulate"
-PREFILL_DTYPE = "fp16 storage; QK and PV 3x f16 hi/lo MFMA, fp32 accumulate"
+PREFILL_DTYPE = ("fp16 storage; QK f16 hi/lo keys x f16 queries (2x f16 MFMA, +1 when a query is not f16-exact), "
+                 "PV f16 values x f16 hi/lo weights (2x f16 MFMA), fp32 accumulate")
 ENCODE_DTYPE = "bf16 in; fp32-exact distances (f16 hi/lo MFMA + exact recount), u8 indices, 2-bit values"
 
 
@@ -150,11 +152,12 @@ def recorded_traffic(name: str, config: dict):
     if not os.path.exists(path):
         return None
     rec = {}
+    keys = ("traffic_bytes_per_launch", *config)
     with open(path) as f:
         for line in f:
-            if "=" in line and line.strip().startswith(("traffic_bytes_per_launch", *config)):
-                k, v = line.split("=", 1)
-                rec[k.strip()] = int(v.strip())
+            m = re.fullmatch(r"\s*(\w+)\s*=\s*(\d+)\s*", line)
+            if m and m.group(1) in keys:
+                rec[m.group(1)] = int(m.group(2))
     if "traffic_bytes_per_launch" not in rec or any(rec.get(k) != v for k, v in config.items()):
         return None
     return rec["traffic_bytes_per_launch"]
@@ -393,7 +396,8 @@ def bench_prefill(args, dev):
                 "head_dim": D, "queries": T, "history": N, "recent": R, "key_format": "block-VQ bd=2 nc=256",
                 "value_bits": 2, "storage_dtype": "fp16", "causal": True},
         roofline={"bound": "mfma", "achieved": achieved, "peak": F16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                  "frac": achieved / F16_PEAK_TFLOPS, "traffic": None,
+                  "frac": achieved / F16_PEAK_TFLOPS,
+                  "traffic": recorded_traffic("prefill_mfma_c4", dict(history=N, queries=T)),
                   "kernel": "prefill_mfma_kernel (history phase, with decode_hist_planes_kernel)",
                   "kernel_ms": kern, "algorithmic_flops": hist_flops, "step_flops": flops,
                   "step_tflops": flops / (ms * 1e-3) / 1e12, "algorithmic_bytes": byts},

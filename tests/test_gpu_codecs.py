@@ -246,6 +246,25 @@ def test_blockvq_encode_parity(dev, dtype, bd):
     assert torch.equal(k_hat, R.blockvq_dequantize(R.BlockQ(got, 128 // bd, bd), Dc))
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_blockvq_encode_eight_blocks(dev, dtype):
+    """head_dim 64 (eight 8-dim blocks): the matrix-core encoder's rows hold
+    fewer than 16 indices, so each token's indices leave byte by byte; odd
+    row counts leave a partly filled last 64-token set."""
+    d, bd = 64, 8
+    Eb, Eib, C, Dc = R.blockvq_fit(sample_keys(4096, d=d, seed=90), sample_keys(4096, d=d, seed=91),
+                                   block_dim=bd, n_centroids=256, iters=5, seed=42)
+    vq = S.SMAQBlockVQ(d, block_dim=bd, device=dev)
+    vq.E_blocks, vq.E_inv_blocks = Eb.to(dev), Eib.to(dev)
+    vq.centroids, vq.decoded_centroids = C.to(dev), Dc.to(dev)
+    keys = sample_keys(2999, d=d, seed=92).to(dtype)
+    ref = R.blockvq_encode(keys, Eb, C).indices
+    vq.tie_counter = _native.TieCounter(dev)
+    got = vq.quantize(keys.to(dev)).indices.cpu().long()
+    assert got.shape == ref.shape == (2999, d // bd)
+    _check_vq_against_oracle(got, ref, keys, Eb, C, vq.tie_counter.value(), f"head_dim 64 {dtype}")
+
+
 def _check_vq_against_oracle(idx_gpu, ref, keys, Eb, C, ties, what):
     """Indices equal the oracle's except at counted argmin ties (distances
     within 1e-6 relative of each other)."""

@@ -42,6 +42,28 @@ def test_prefill_scalar_vs_oracle(dev, causal):
     assert_attn_close(out, R.hybrid_attention(q, ref, kr, vr, hq, query_positions=pos), f"prefill causal={causal}")
 
 
+def test_prefill_f16_values_within_bound(dev):
+    """The matrix-core prefill feeds the history values to the matrix ops
+    rounded to f16 (11 significant bits), so an output may move by up to
+    2^-11 max|v| from the fp32 path.  With fp32 queries neither side rounds
+    the output; values of scale 8 (|v| up to ~35, where the bound is several
+    times the default 2e-3) must stay within it (+5% for the ~22-bit scores'
+    share).  A bf16 value plane (8 bits) would fail it."""
+    hkv, hq, N, T = 2, 8, 900, 64
+    st, ref = _pair_scalar(dev, bits=4, hkv=hkv)
+    keys = sample_keys(N * hkv, seed=231).reshape(N, hkv, 128)
+    vals = 8 * torch.randn(N, hkv, 128, generator=torch.Generator().manual_seed(232))
+    st.append_chunk(keys.to(dev), vals.to(dev))
+    ref.append_chunk(keys, vals)
+    q = sample_keys(T * hq, seed=233).reshape(T, hq, 128)
+    out = S.compute_hybrid_attention(q.to(dev), st, None, None, hq, impl=3).float().cpu()
+    want = R.hybrid_attention(q, ref, None, None, hq)
+    vmax = R.dequantize_values(ref.get_flat_cache().value_q).abs().max().item()
+    err = (out - want).abs().max().item()
+    print(f"\n[f16 values] max|err|={err:.3e} bound={2.0 ** -11 * vmax:.3e} (max|v|={vmax:.2f})")
+    assert vmax > 16 and err <= 1.05 * 2.0 ** -11 * vmax, (err, vmax)
+
+
 def test_prefill_blockvq_vs_oracle(dev):
     """c4 format: block-VQ keys (block_dim 2, 256 centroids) with outlier
     channels, fp16 recent window, 130 causal fp16 queries at the end."""

@@ -35,10 +35,15 @@
 //   softmax per query column (keys = C rows: 4 per lane, 4 lane groups)
 //   O^T[dim][query] += V^T . P^T  A = value rows (dimension-major tile),
 //                                B = P^T straight from the S^T accumulators
-// with qh.kh + qh.kl + ql.kh and v.ph + v.pl.  Each workgroup (8
-// waves x 32 query rows) streams the 64-key tiles of one (sequence, query
-// head, key split), double-buffered: the next tile is copied straight into
-// LDS (global_load_lds_dwordx4) while the current one is computed.  It writes
+// with qh.kh + qh.kl + ql.kh (ql.kh skipped where every query lo part is
+// zero).  The weights p enter PV at the precision of the output type: as
+// v.ph + v.pl (~22 bits) for an fp32 output; as v.ph alone (f16, 11 bits)
+// for an fp16 or bf16 output, whose own rounding is 2^-11 or 2^-8 relative.
+// Rounding p moves an output by at most 2^-11 sum w|v| more (w = p / l, l
+// summed from the unrounded weights), as the value rounding above does.
+// Each workgroup (8 waves x 32 query rows) streams the 64-key tiles of one
+// (sequence, query head, key split) through a ring of three LDS buffers,
+// copied straight into LDS (global_load_lds_dwordx4) two tiles ahead.  It writes
 // the same (m, l, o) partials as the other attention kernels;
 // attn_combine_kernel merges splits and the history / recent parts.
 #include <math.h>
@@ -96,6 +101,11 @@ __device__ __forceinline__ void split2_f16(float x0, float x1, float one, uint32
   const f32x2 r = {__builtin_fmaf(one, x0, -(float)h[0]), __builtin_fmaf(one, x1, -(float)h[1])};
   hi = __builtin_bit_cast(uint32_t, h);
   lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, f16x2));
+}
+
+// two numbers rounded to f16 in one packed convert
+__device__ __forceinline__ uint32_t pack2_f16(float x0, float x1) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){x0, x1}, f16x2));
 }
 
 __device__ __forceinline__ int exponent_of(float x) {
@@ -266,7 +276,7 @@ __global__ __launch_bounds__(256) void decode_recent_planes_kernel(smaq_attn_par
 
 // --------------------------------------------------------------- kernel ----
 // grid: x = key split, y = query head, z = sequence * query blocks
-template <bool CAUSAL>
+template <bool CAUSAL, bool P_LO>
 __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_mfma_kernel(
     smaq_attn_params p, PrefillPart pp, Partials part) {
   __shared__ __attribute__((aligned(16))) _Float16 tiles[3][kImg];   // ring of three tile images
@@ -492,7 +502,10 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[qb][kb][v + 1], qfac[qb], mneg));
             ls += p0 + p1;
             const int dw = 2 * (kb & 1) + (v >> 1);
-            split2_f16(p0, p1, one, hw[kb >> 1][dw], lw[kb >> 1][dw]);
+            if constexpr (P_LO)
+              split2_f16(p0, p1, one, hw[kb >> 1][dw], lw[kb >> 1][dw]);
+            else
+              hw[kb >> 1][dw] = pack2_f16(p0, p1);
           }
       } else {
 #pragma unroll
@@ -506,14 +519,17 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             const float p1 = dead ? 0.0f : __builtin_amdgcn_exp2f(x1 - m_run[qb]);
             ls += p0 + p1;
             const int dw = 2 * (kb & 1) + (v >> 1);
-            split2_f16(p0, p1, one, hw[kb >> 1][dw], lw[kb >> 1][dw]);
+            if constexpr (P_LO)
+              split2_f16(p0, p1, one, hw[kb >> 1][dw], lw[kb >> 1][dw]);
+            else
+              hw[kb >> 1][dw] = pack2_f16(p0, p1);
           }
       }
       l_run[qb] += ls;
 #pragma unroll
       for (int st = 0; st < 2; ++st) {
         ph[qb][st] = u32x4{hw[st][0], hw[st][1], hw[st][2], hw[st][3]};
-        pl[qb][st] = u32x4{lw[st][0], lw[st][1], lw[st][2], lw[st][3]};
+        if constexpr (P_LO) pl[qb][st] = u32x4{lw[st][0], lw[st][1], lw[st][2], lw[st][3]};
       }
     }
     // ---- O^T += V^T P^T: dims 16db + 4kg + v (rows), query column n
@@ -530,8 +546,9 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int qb = 0; qb < 2; ++qb) {
           acc_o[qb][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av),
                                                                  __builtin_bit_cast(f16x8, ph[qb][st]), acc_o[qb][db], 0, 0, 0);
-          acc_o[qb][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av),
-                                                                 __builtin_bit_cast(f16x8, pl[qb][st]), acc_o[qb][db], 0, 0, 0);
+          if constexpr (P_LO)
+            acc_o[qb][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av),
+                                                                   __builtin_bit_cast(f16x8, pl[qb][st]), acc_o[qb][db], 0, 0, 0);
         }
       }
     __builtin_amdgcn_s_setprio(0);
@@ -650,10 +667,16 @@ int launch_prefill_mfma(const smaq_attn_params& p, const PrefillPart& pp, int n_
                         hipStream_t st) {
   const int nqb = (p.q_len + kQB - 1) / kQB;
   dim3 grid((unsigned)n_splits, p.n_q_heads, (unsigned)(p.batch * nqb));
-  if (p.q_positions)
-    hipLaunchKernelGGL(prefill_mfma_kernel<true>, grid, dim3(kPT), 0, st, p, pp, part);
+  // weights hi/lo for fp32 outputs, f16 weights for fp16 / bf16 outputs
+  const bool p_lo = p.out_dtype == SMAQ_F32;
+  if (p.q_positions && p_lo)
+    hipLaunchKernelGGL((prefill_mfma_kernel<true, true>), grid, dim3(kPT), 0, st, p, pp, part);
+  else if (p.q_positions)
+    hipLaunchKernelGGL((prefill_mfma_kernel<true, false>), grid, dim3(kPT), 0, st, p, pp, part);
+  else if (p_lo)
+    hipLaunchKernelGGL((prefill_mfma_kernel<false, true>), grid, dim3(kPT), 0, st, p, pp, part);
   else
-    hipLaunchKernelGGL(prefill_mfma_kernel<false>, grid, dim3(kPT), 0, st, p, pp, part);
+    hipLaunchKernelGGL((prefill_mfma_kernel<false, false>), grid, dim3(kPT), 0, st, p, pp, part);
   return launch_status("smaq_attn_hybrid(prefill)");
 }
 

@@ -64,6 +64,28 @@ def test_prefill_f16_values_within_bound(dev):
     assert vmax > 16 and err <= 1.05 * 2.0 ** -11 * vmax, (err, vmax)
 
 
+def test_prefill_f16_output_weights_within_bound(dev):
+    """For an fp16 output the weights also enter the matrix ops as f16, one
+    more 2^-11 sum w|v| (the output's own rounding is 2^-11 |o| <= 2^-11
+    max|v|): three such terms against the fp32 path on the same f16-exact
+    queries.  Weights rounded to bf16 (8 bits) would exceed it."""
+    hkv, hq, N, T = 2, 8, 900, 64
+    st, ref = _pair_scalar(dev, bits=4, hkv=hkv)
+    keys = sample_keys(N * hkv, seed=241).reshape(N, hkv, 128)
+    vals = 8 * torch.randn(N, hkv, 128, generator=torch.Generator().manual_seed(242))
+    st.append_chunk(keys.to(dev), vals.to(dev))
+    ref.append_chunk(keys, vals)
+    q = sample_keys(T * hq, seed=243).reshape(T, hq, 128).half()
+    out = S.compute_hybrid_attention(q.to(dev), st, None, None, hq, impl=3)
+    assert out.dtype == torch.float16
+    want = R.hybrid_attention(q.float(), ref, None, None, hq)
+    vmax = R.dequantize_values(ref.get_flat_cache().value_q).abs().max().item()
+    err = (out.float().cpu() - want).abs().max().item()
+    bound = 3 * 2.0 ** -11 * vmax
+    print(f"\n[f16 weights] max|err|={err:.3e} bound={bound:.3e} (max|v|={vmax:.2f})")
+    assert vmax > 16 and err <= 1.05 * bound, (err, vmax)
+
+
 def test_prefill_blockvq_vs_oracle(dev):
     """c4 format: block-VQ keys (block_dim 2, 256 centroids) with outlier
     channels, fp16 recent window, 130 causal fp16 queries at the end."""

@@ -469,12 +469,18 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           for (int v = 0; v < 4; ++v) mt = fmaxf(mt, sacc[qb][kb][v]);
         mt *= qfac[qb];
       } else {
+        // (opaque copies keep the compiler from computing this branch's
+        // products and compares on the unmasked tiles as well, to share
+        // them with the masked weights below)
+        float qf = qfac[qb];
+        int lm = lim;
+        asm volatile("" : "+v"(qf), "+v"(lm));
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
-            const float x = sacc[qb][kb][v] * qfac[qb];
-            mt = fmaxf(mt, 16 * kb + 4 * kg + v >= lim ? -__builtin_inff() : x);
+            const float x = sacc[qb][kb][v] * qf;
+            mt = fmaxf(mt, 16 * kb + 4 * kg + v >= lm ? -__builtin_inff() : x);
           }
       }
       mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
@@ -508,13 +514,16 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
               hw[kb >> 1][dw] = pack2_f16(p0, p1);
           }
       } else {
+        float qf = qfac[qb];
+        int lm = lim;
+        asm volatile("" : "+v"(qf), "+v"(lm));
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
           for (int v = 0; v < 4; v += 2) {
-            float x0 = sacc[qb][kb][v] * qfac[qb], x1 = sacc[qb][kb][v + 1] * qfac[qb];
-            if (16 * kb + 4 * kg + v >= lim) x0 = -__builtin_inff();
-            if (16 * kb + 4 * kg + v + 1 >= lim) x1 = -__builtin_inff();
+            float x0 = sacc[qb][kb][v] * qf, x1 = sacc[qb][kb][v + 1] * qf;
+            if (16 * kb + 4 * kg + v >= lm) x0 = -__builtin_inff();
+            if (16 * kb + 4 * kg + v + 1 >= lm) x1 = -__builtin_inff();
             const float p0 = dead ? 0.0f : __builtin_amdgcn_exp2f(x0 - m_run[qb]);
             const float p1 = dead ? 0.0f : __builtin_amdgcn_exp2f(x1 - m_run[qb]);
             ls += p0 + p1;

@@ -457,10 +457,18 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // the masked form.
     u32x4 ph[2][2], pl[2][2];  // [qb][32-key step]: P^T as B operands
     const bool plain = __all(kt0 + kKT <= vis[0] && kt0 + kKT <= vis[1]);
+    // Keys kt0 + i are visible to column qb for i < lim_of(qb).  The masked
+    // branches below take opaque copies of the scale and of vis: the
+    // compiler otherwise computes their products, compares and limits on the
+    // unmasked tiles as well, to share them between the masked maximum and
+    // the masked weights.
+    auto lim_of = [&](int qb) -> int {
+      int64_t vv = vis[qb];
+      asm volatile("" : "+v"(vv));
+      return (int)max((int64_t)-1, min((int64_t)kKT, vv - kt0));
+    };
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
-      // keys kt0 + i are visible to this column for i < lim
-      const int lim = (int)max((int64_t)-1, min((int64_t)kKT, vis[qb] - kt0));
       float mt = -__builtin_inff();
       if (plain) {
 #pragma unroll
@@ -469,12 +477,9 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           for (int v = 0; v < 4; ++v) mt = fmaxf(mt, sacc[qb][kb][v]);
         mt *= qfac[qb];
       } else {
-        // (opaque copies keep the compiler from computing this branch's
-        // products and compares on the unmasked tiles as well, to share
-        // them with the masked weights below)
         float qf = qfac[qb];
-        int lm = lim;
-        asm volatile("" : "+v"(qf), "+v"(lm));
+        asm volatile("" : "+v"(qf));
+        const int lm = lim_of(qb);
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
@@ -515,8 +520,8 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           }
       } else {
         float qf = qfac[qb];
-        int lm = lim;
-        asm volatile("" : "+v"(qf), "+v"(lm));
+        asm volatile("" : "+v"(qf));
+        const int lm = lim_of(qb);
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb)
 #pragma unroll

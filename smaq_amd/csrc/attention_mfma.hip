@@ -248,15 +248,43 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
   constexpr uint32_t kMask = (1u << KBITS) - 1u;
   constexpr float kLog2e = 1.4426950408889634f;
 
+  // The prologue's two global reads (the query rows, the key centroids) are
+  // issued together: the query rows first, as vector loads; the centroids as
+  // scalar loads, each lane taking its table entries from them by index.
+  const int qrow = n < Q ? n : ((n >= 8 && n < 8 + Q) ? n - 8 : -1);
+  const float* qsrc = p.q_hist + ((int64_t)b * p.n_q_heads + h * Q + (qrow < 0 ? 0 : qrow)) * 128;
+  // (padding columns read query row 0 and drop it: loads without a branch)
+  float qv[32];
+#pragma unroll
+  for (int i = 0; i < 32; i += 4) {
+    const float4 v4 = *(const float4*)(qsrc + 32 * kg + i);
+    qv[i] = v4.x; qv[i + 1] = v4.y; qv[i + 2] = v4.z; qv[i + 3] = v4.w;
+  }
+#pragma unroll
+  for (int i = 0; i < 32; ++i) qv[i] = qrow < 0 ? 0.0f : qv[i];
+  float cent[1 << KBITS];
+  typedef const __attribute__((address_space(4))) float* ConstFloatPtr;
+  const ConstFloatPtr klut = (ConstFloatPtr)p.key_lut;
+#pragma unroll
+  for (int i = 0; i < (1 << KBITS); ++i) cent[i] = klut[i];
+
   // ---- key LUT: byte (c0 | c1 << KBITS) -> packed f16 hi / lo of both codes,
   // centroids pre-scaled by 2^-e_lut so the largest has magnitude in [1, 2)
   float cmax = 0.0f;
-  for (int i = 0; i < (1 << KBITS); ++i) cmax = fmaxf(cmax, fabsf(p.key_lut[i]));
+#pragma unroll
+  for (int i = 0; i < (1 << KBITS); ++i) cmax = fmaxf(cmax, fabsf(cent[i]));
   const int e_lut = exponent_of(cmax);
   const float lut_scale = ldexpf(1.0f, -e_lut);
-  for (int v = tid; v < 256; v += 256) {
-    const float c0 = p.key_lut[v & kMask] * lut_scale;
-    const float c1 = p.key_lut[(v >> KBITS) & kMask] * lut_scale;
+  {
+    const int v = tid;  // 256 threads, one entry each
+    float c0 = cent[0], c1 = cent[0];
+#pragma unroll
+    for (int i = 1; i < (1 << KBITS); ++i) {
+      c0 = (v & kMask) == (uint32_t)i ? cent[i] : c0;
+      c1 = ((v >> KBITS) & kMask) == (uint32_t)i ? cent[i] : c1;
+    }
+    c0 *= lut_scale;
+    c1 *= lut_scale;
     const _Float16 h0 = (_Float16)c0, h1 = (_Float16)c1;
     const _Float16 l0 = (_Float16)(c0 - (float)h0), l1 = (_Float16)(c1 - (float)h1);
     lut[v] = u32x2{f16_bits(h0) | (f16_bits(h1) << 16), f16_bits(l0) | (f16_bits(l1) << 16)};
@@ -264,15 +292,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
 
   // ---- query B operands: columns [0, Q) hold the hi parts of query rows
   // 0..Q-1, columns [8, 8+Q) their lo parts, the rest zero
-  const int qrow = n < Q ? n : ((n >= 8 && n < 8 + Q) ? n - 8 : -1);
-  const float* qsrc = p.q_hist + ((int64_t)b * p.n_q_heads + h * Q + (qrow < 0 ? 0 : qrow)) * 128;
-  float qv[32];
   float qmax = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    qv[i] = qrow < 0 ? 0.0f : qsrc[32 * kg + i];
-    qmax = fmaxf(qmax, fabsf(qv[i]));
-  }
+  for (int i = 0; i < 32; ++i) qmax = fmaxf(qmax, fabsf(qv[i]));
   qmax = fmaxf(qmax, __shfl_xor(qmax, 16, 64));
   qmax = fmaxf(qmax, __shfl_xor(qmax, 32, 64));
   const int e_q = exponent_of(qmax);

@@ -43,7 +43,9 @@
 // summed from the unrounded weights), as the value rounding above does.
 // Each workgroup (8 waves x 32 query rows) streams the 64-key tiles of one
 // (sequence, query head, key split) through a ring of three LDS buffers,
-// copied straight into LDS (global_load_lds_dwordx4) two tiles ahead.  It writes
+// copied straight into LDS (global_load_lds_dwordx4) one tile ahead; the
+// second wave of every SIMD runs its PV one tile late, so that the two
+// waves' matrix and vector phases interleave.  It writes
 // the same (m, l, o) partials as the other attention kernels;
 // attn_combine_kernel merges splits and the history / recent parts.
 #include <math.h>
@@ -70,8 +72,6 @@ constexpr int kImg = 8192 * kPrefillPlanes;  // halves per tile image (48 KB)
 constexpr int kImgKL = 8192, kImgV = 16384;   // part offsets (halves)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kCopyLoads = kImg * 2 / 16 / kPT;  // 16-byte direct-to-LDS loads per thread and tile
-// s_waitcnt immediate: vmcnt <= kCopyLoads, expcnt and lgkmcnt not waited
-constexpr int kWaitTileAhead = (15 << 8) | (7 << 4) | kCopyLoads;
 static_assert(kCopyLoads == 6 && kImg * 2 == kCopyLoads * 16 * kPT, "tile copy: whole 16-byte loads per thread");
 constexpr float kLazy = 8.0f;     // softmax reference max raised by > 2^8 only
 
@@ -387,30 +387,57 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                                        (__attribute__((address_space(3))) void*)(&tiles[buf][8 * unit0]), 16, 0, 0);
     }
   };
-  // tiles i + 1 and i + 2 are in flight while tile i is computed
+  // Waves w and w + 4 of the workgroup share a SIMD.  Waves 0-3 run tile i
+  // as QK(i), softmax(i), PV(i); waves 4-7 as PV(i - 1), QK(i), softmax(i),
+  // so that on every SIMD one wave's softmax runs beside the other's matrix
+  // work rather than in step with it.  The ring then holds tiles i - 1, i
+  // and (arriving) i + 1 while tile i is computed: tile i + 1 is copied
+  // into the buffer of tile i - 2 once every wave has passed tile i's
+  // barrier.
+  const bool late = wu >= 4;
   if (k0 < k1) copy_tile(k0, 0);
-  if (k0 + kKT < k1) copy_tile(k0 + kKT, 1);
   float one = 1.0f;  // opaque to the compiler (see split2_f16)
   asm volatile("" : "+v"(one));
-  int buf = 0;  // ring buffer of tile i
+  u32x4 ph[2][2], pl[2][2];  // [qb][32-key step]: P^T as B operands
+  // ---- O^T += V^T P^T over the value image vimg: dims 16db + 4kg + v
+  // (rows), query column n
+  auto pv = [&](const _Float16* vimg) {
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int db = 0; db < 8; ++db) {
+        // A: dim 16db + n, keys 32st + 4kg + 0..3 and 32st + 16 + 4kg + 0..3
+        // (one unit of the value image)
+        const int off = vimg_off(16 * db + n, 4 * st + kg);
+        const u32x4 av = *(const u32x4*)&vimg[off];
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+          acc_o[qb][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av),
+                                                                 __builtin_bit_cast(f16x8, ph[qb][st]), acc_o[qb][db], 0, 0, 0);
+          if constexpr (P_LO)
+            acc_o[qb][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av),
+                                                                   __builtin_bit_cast(f16x8, pl[qb][st]), acc_o[qb][db], 0, 0, 0);
+        }
+      }
+    __builtin_amdgcn_s_setprio(0);
+  };
+  int buf = 0;  // ring buffer of tile i (tile i - 1 sits in buf - 1 mod 3)
   for (int64_t kt0 = k0; kt0 < k1; kt0 += kKT) {
-    // this thread's copies of tile i have landed (copies complete in order;
-    // only tile i + 1's kCopyLoads may still be in flight), then every
-    // thread's have, and every wave is done with tile i - 1, whose buffer
-    // takes tile i + 2.  The barrier carries no memory fence (which would
-    // wait for tile i + 1 too); the empty asm statements keep the compiler
-    // from moving LDS accesses across it.
-    if (kt0 + kKT < k1)
-      __builtin_amdgcn_s_waitcnt(kWaitTileAhead);
-    else
-      __builtin_amdgcn_s_waitcnt(0);
+    // this thread's copies of tile i have landed, then every thread's have,
+    // and every wave is done with tile i - 2, whose buffer takes tile i + 1.
+    // The barrier carries no memory fence; the empty asm statements keep
+    // the compiler from moving LDS accesses across it.
+    __builtin_amdgcn_s_waitcnt(0);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (kt0 + 2 * kKT < k1) copy_tile(kt0 + 2 * kKT, buf == 0 ? 2 : buf - 1);
+    const int nbuf = buf == 2 ? 0 : buf + 1;
+    if (kt0 + kKT < k1) copy_tile(kt0 + kKT, nbuf);
     const _Float16* kimg = tiles[buf];
     const _Float16* vimg = tiles[buf] + kImgV;
-    buf = buf == 2 ? 0 : buf + 1;
+    if (late && kt0 > k0) pv(tiles[buf == 0 ? 2 : buf - 1] + kImgV);
+    buf = nbuf;
     // ---- S^T = K Q^T: keys 16kb + 4kg + v (rows), query 16qb + n (column)
     f32x4 sacc[2][4];
 #pragma unroll
@@ -455,7 +482,6 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // commutes with it) and a weight is exp2(s qfac - m), one fused
     // multiply-add; boundary tiles and columns with no visible key yet take
     // the masked form.
-    u32x4 ph[2][2], pl[2][2];  // [qb][32-key step]: P^T as B operands
     const bool plain = __all(kt0 + kKT <= vis[0] && kt0 + kKT <= vis[1]);
     // Keys kt0 + i are visible to column qb for i < lim_of(qb).  The masked
     // branches below take opaque copies of the scale and of vis: the
@@ -546,27 +572,10 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         if constexpr (P_LO) pl[qb][st] = u32x4{lw[st][0], lw[st][1], lw[st][2], lw[st][3]};
       }
     }
-    // ---- O^T += V^T P^T: dims 16db + 4kg + v (rows), query column n
-    __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-    for (int st = 0; st < 2; ++st)
-#pragma unroll
-      for (int db = 0; db < 8; ++db) {
-        // A: dim 16db + n, keys 32st + 4kg + 0..3 and 32st + 16 + 4kg + 0..3
-        // (one unit of the value image)
-        const int off = vimg_off(16 * db + n, 4 * st + kg);
-        const u32x4 av = *(const u32x4*)&vimg[off];
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-          acc_o[qb][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av),
-                                                                 __builtin_bit_cast(f16x8, ph[qb][st]), acc_o[qb][db], 0, 0, 0);
-          if constexpr (P_LO)
-            acc_o[qb][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av),
-                                                                   __builtin_bit_cast(f16x8, pl[qb][st]), acc_o[qb][db], 0, 0, 0);
-        }
-      }
-    __builtin_amdgcn_s_setprio(0);
+    if (!late) pv(vimg);
   }
+  // the late waves' PV of the last tile (its buffer is not copied over again)
+  if (late && k0 < k1) pv(tiles[buf == 0 ? 2 : buf - 1] + kImgV);
 
   // ---- partials (natural-log max), one row per valid query column
 #pragma unroll

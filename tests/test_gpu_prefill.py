@@ -42,6 +42,28 @@ def test_prefill_scalar_vs_oracle(dev, causal):
     assert_attn_close(out, R.hybrid_attention(q, ref, kr, vr, hq, query_positions=pos), f"prefill causal={causal}")
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_single_tile_parts(dev, causal, dtype):
+    """History and recent window of one 64-key tile each (40 + 20 tokens),
+    24 queries: each workgroup's loop runs once, so the waves that take
+    their PV one tile late do it after the loop."""
+    hkv, hq, N, Rn, T = 2, 8, 40, 20, 24
+    st, ref = _pair_scalar(dev, bits=4, hkv=hkv)
+    keys = sample_keys(N * hkv, seed=251).reshape(N, hkv, 128)
+    vals = torch.randn(N, hkv, 128, generator=torch.Generator().manual_seed(252))
+    st.append_chunk(keys.to(dev), vals.to(dev))
+    ref.append_chunk(keys, vals)
+    q = sample_keys(T * hq, seed=253).reshape(T, hq, 128).to(dtype)
+    kr = sample_keys(Rn * hkv, seed=254).reshape(Rn, hkv, 128).to(dtype)
+    vr = torch.randn(Rn, hkv, 128, generator=torch.Generator().manual_seed(255)).to(dtype)
+    pos = torch.arange(N + Rn - T, N + Rn) if causal else None
+    out = S.compute_hybrid_attention(q.to(dev), st, kr.to(dev), vr.to(dev), hq,
+                                     query_positions=None if pos is None else pos.to(dev), impl=3)
+    assert_attn_close(out, R.hybrid_attention(q, ref, kr, vr, hq, query_positions=pos),
+                      f"prefill one tile causal={causal} {dtype}")
+
+
 def test_prefill_f16_values_within_bound(dev):
     """The matrix-core prefill feeds the history values to the matrix ops
     rounded to f16 (11 significant bits), so an output may move by up to

@@ -785,9 +785,10 @@ bool mfma_decode_supported(const smaq_attn_params& p) {
          p.key_row_bytes == 64 && p.val_bits == 2 && p.val_group == 32 && p.val_row_bytes == 32 &&
          g >= 1 && g <= 4 &&
          (!p.block_table || (p.block_size >= 16 && (p.block_size & (p.block_size - 1)) == 0)) &&
-         // vector loads of rows and row pairs assume 16-byte aligned arrays
+         // vector loads of rows, row pairs and query rows assume 16-byte
+         // aligned arrays
          (((uintptr_t)p.key_bytes | (uintptr_t)p.val_bytes | (uintptr_t)p.key_norms |
-           (uintptr_t)p.val_scales | (uintptr_t)p.val_zeros) & 15) == 0;
+           (uintptr_t)p.val_scales | (uintptr_t)p.val_zeros | (uintptr_t)p.q_hist) & 15) == 0;
 }
 
 // Sequences by history length, longest first: a counting sort on 1024

@@ -53,6 +53,9 @@ struct PrefillPart {
   int s_base;                   // first partials split of this part
 };
 
+// compute units of the current device (256 if the query fails)
+int device_cu_count();
+
 bool prefill_mfma_supported(const smaq_attn_params& p);
 int64_t prefill_padded_len(int64_t L);
 int64_t prefill_split_len(const smaq_attn_params& p, int64_t L);

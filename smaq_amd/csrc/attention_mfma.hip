@@ -831,9 +831,16 @@ int launch_decode_order(const smaq_attn_params& p, int* order, hipStream_t st) {
   return launch_status("smaq_attn_hybrid(decode order)");
 }
 
+// Contexts are split so that the grid fills one round of the device's
+// workgroup slots (kDecodeWaves workgroups of 4 waves per CU): a workgroup's
+// fixed costs (its prologue and first tile's latency, the 4-wave merge) are
+// then paid once per slot (c3: 4 splits, 1024 workgroups, 0.177 ms against
+// 0.183 ms for two rounds of half the length).
 int64_t mfma_decode_split_len(const smaq_attn_params& p) {
   const int64_t units = (int64_t)p.batch * p.n_kv_heads;
-  const int64_t want = units >= 2048 ? 1 : (2048 + units - 1) / units;
+  const bool wide = p.norm_dtype == SMAQ_F32 || p.val_dtype == SMAQ_F32;
+  const int64_t slots = (int64_t)device_cu_count() * (wide ? 3 : 4);
+  const int64_t want = units >= slots ? 1 : (slots + units - 1) / units;
   int64_t split = (p.max_hist_len + want - 1) / want;
   const int64_t q = kMWaves * kMTile;
   split = ((split + q - 1) / q) * q;

@@ -612,20 +612,20 @@ bool prefill_mfma_supported(const smaq_attn_params& p) {
 
 int64_t prefill_padded_len(int64_t L) { return ((L + kKT - 1) / kKT) * kKT; }
 
-// Workgroups hold 96 KB of LDS, one per CU.  Split the keys so that the
+int device_cu_count() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) == hipSuccess &&
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
+    return cus;
+  return 256;
+}
+
+// Workgroups hold 144 KB of LDS, one per CU.  Split the keys so that the
 // grid covers at least three rounds of the device's CUs and, among up to
 // twice that many splits, the one whose last round is fullest (splits of at
 // least four tiles).
 int64_t prefill_split_len(const smaq_attn_params& p, int64_t L) {
-  static int n_cu = 0;
-  if (n_cu <= 0) {
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
-      n_cu = cus;
-    else
-      n_cu = 256;
-  }
+  const int n_cu = device_cu_count();
   const int64_t wgs = (int64_t)p.batch * p.n_q_heads * ((p.q_len + kQB - 1) / kQB);
   const int64_t max_s = (L + 4 * kKT - 1) / (4 * kKT);
   const int64_t s_min = std::min(max_s, std::max<int64_t>(1, (3 * n_cu + wgs - 1) / wgs));

@@ -52,6 +52,37 @@ constexpr int kARow = 144;  // bytes per row of the staged PV A operand (64 hi +
 // The softmax reference maximum is raised only when a score exceeds it by
 // this much (log2 units), so weights stay below 2^8 and rescales are rare.
 constexpr float kLazyRescale = 8.0f;
+// s_waitcnt operand that waits for LDS and scalar loads only (lgkmcnt 0,
+// vmcnt and expcnt at their maxima)
+constexpr int kWaitLdsOnly = 0xC07F;
+
+// Split boundaries.  The grid (KV heads, sequences, splits) is dispatched
+// split-major, so with one round of workgroups, split s of unit u = head +
+// n_kv_heads * sequence runs in round-slot k = (u + units * s) / n_cu of its
+// CU.  A CU's
+// memory pipeline serves its earlier-dispatched workgroups first: with equal
+// splits (c3 on MI355X, 4 slots per CU) the slots took 147, 154, 162 and
+// 169 us.  Split s therefore weighs kSplitWeight - tilt * k, and its first
+// token is the sequence length times the weight of the splits before it over
+// the total, rounded down to whole 128-token steps.
+struct SplitRule {
+  int n_splits;
+  int n_cu;   // workgroups per round-slot (the device's CU count)
+  int slots;  // round-slots per CU
+  int tilt;   // weight step per slot; tilt * (slots - 1) < kSplitWeight
+};
+constexpr int kSplitWeight = 64;
+
+// Weight of splits 0 .. s-1 of unit u (of `units`).
+__device__ __forceinline__ int split_weight_before(const SplitRule& r, int u, int units, int s) {
+  int c = kSplitWeight * s;
+  for (int j = 1; j < r.slots; ++j) {
+    const int num = j * r.n_cu - u;  // splits >= first run in slot j or later
+    const int first = num <= 0 ? 0 : (int)(((unsigned)num + (unsigned)units - 1u) / (unsigned)units);
+    c -= r.tilt * (s > first ? s - first : 0);
+  }
+  return c;
+}
 
 // Rows of one 32-token tile: tokens 0..15 at rows gA.., 16..31 at gB..
 struct TileDesc {
@@ -219,7 +250,7 @@ struct NormPair {
 
 template <int KBITS, typename TN, typename TV, bool SPLIT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWaves<TN, TV>, kDecodeWaves<TN, TV>))) void decode_mfma_kernel(
-    smaq_attn_params p, HistAddr addr, Partials part, int64_t split_len, const int* __restrict__ order) {
+    smaq_attn_params p, HistAddr addr, Partials part, SplitRule rule, const int* __restrict__ order) {
   // key LUT, one 8-byte entry per code byte: {f16 hi pair, f16 lo pair}
   // (read with ds_read_b64, twice the rate of two dword reads)
   __shared__ __attribute__((aligned(16))) u32x2 lut[256];
@@ -234,7 +265,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
   // per-wave results, laid over the spread tiles once every wave has left its loop
   float (*const red_o)[4][128] = (float (*)[4][128])&vsp[0][0];
 
-  const int tid = threadIdx.x;
+  // Thread and workgroup ids come from the hardware registers directly: this
+  // file is built without IEEE mode, which keeps the device library's
+  // accessors (threadIdx, blockIdx) from being inlined.
+  const int tid = (int)__builtin_amdgcn_workitem_id_x();
+  const int gx = (int)__builtin_amdgcn_workgroup_id_x(), gy = (int)__builtin_amdgcn_workgroup_id_y();
+  const int gz = (int)__builtin_amdgcn_workgroup_id_z();
   const int lane = tid & 63, w = tid >> 6;
   const int wu = __builtin_amdgcn_readfirstlane(w);  // wave index, in an SGPR
   const int n = lane & 15, kg = lane >> 4;           // MFMA lane coordinates
@@ -242,8 +278,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
   // this lane's two softmax tokens: C-layout values 2*bank, 2*bank + 1
   const int tokA = bank < 2 ? 4 * kg + 2 * bank : 16 + 4 * kg + 2 * (bank - 2);
   const int tq = lane & 7, pq = lane >> 3;           // value loader: tokens 4tq.., bytes 4pq..
-  const int s = blockIdx.x, h = blockIdx.y;
-  const int b = order ? __builtin_amdgcn_readfirstlane(order[blockIdx.z]) : (int)blockIdx.z;
+  const int s = gz, h = gx;
+  // per-sequence lookups go through the scalar cache (no vector-memory wait
+  // in the prologue)
+  typedef const __attribute__((address_space(4))) int* ConstIntPtr;
+  typedef const __attribute__((address_space(4))) int64_t* ConstI64Ptr;
+  const int b = order ? ((ConstIntPtr)order)[gy] : gy;
   const int Q = p.n_q_heads / p.n_kv_heads;  // query rows (decode: one token)
   constexpr uint32_t kMask = (1u << KBITS) - 1u;
   constexpr float kLog2e = 1.4426950408889634f;
@@ -268,112 +308,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
 #pragma unroll
   for (int i = 0; i < (1 << KBITS); ++i) cent[i] = klut[i];
 
-  // ---- key LUT: byte (c0 | c1 << KBITS) -> packed f16 hi / lo of both codes,
-  // centroids pre-scaled by 2^-e_lut so the largest has magnitude in [1, 2)
-  float cmax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < (1 << KBITS); ++i) cmax = fmaxf(cmax, fabsf(cent[i]));
-  const int e_lut = exponent_of(cmax);
-  const float lut_scale = ldexpf(1.0f, -e_lut);
-  {
-    const int v = tid;  // 256 threads, one entry each
-    float c0 = cent[0], c1 = cent[0];
-#pragma unroll
-    for (int i = 1; i < (1 << KBITS); ++i) {
-      c0 = (v & kMask) == (uint32_t)i ? cent[i] : c0;
-      c1 = ((v >> KBITS) & kMask) == (uint32_t)i ? cent[i] : c1;
-    }
-    c0 *= lut_scale;
-    c1 *= lut_scale;
-    const _Float16 h0 = (_Float16)c0, h1 = (_Float16)c1;
-    const _Float16 l0 = (_Float16)(c0 - (float)h0), l1 = (_Float16)(c1 - (float)h1);
-    lut[v] = u32x2{f16_bits(h0) | (f16_bits(h1) << 16), f16_bits(l0) | (f16_bits(l1) << 16)};
+  // ---- split range: split s of this sequence and head holds
+  // tokens [s0, s1) (wave-uniform values are pinned to SGPRs so the tile
+  // loop's control flow and address arithmetic stay scalar)
+  const int64_t len =
+      uniform64(p.hist_len ? min(((ConstI64Ptr)p.hist_len)[b], (int64_t)p.max_hist_len) : p.max_hist_len);
+  int64_t s0 = 0, s1 = len;
+  if (rule.n_splits > 1) {
+    // (a shared boundary is computed by the same expression for both of its
+    // splits, so rounding cannot open a gap or an overlap)
+    const int units = p.n_kv_heads * p.batch, u = h + p.n_kv_heads * gy;
+    const double per_weight = (double)len / (double)split_weight_before(rule, u, units, rule.n_splits);
+    constexpr int64_t kStepMask = ~(int64_t)(kMWaves * kMTile - 1);
+    if (s > 0) s0 = (int64_t)(per_weight * split_weight_before(rule, u, units, s)) & kStepMask;
+    if (s + 1 < rule.n_splits) s1 = (int64_t)(per_weight * split_weight_before(rule, u, units, s + 1)) & kStepMask;
   }
-
-  // ---- query B operands: columns [0, Q) hold the hi parts of query rows
-  // 0..Q-1, columns [8, 8+Q) their lo parts, the rest zero
-  float qmax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 32; ++i) qmax = fmaxf(qmax, fabsf(qv[i]));
-  qmax = fmaxf(qmax, __shfl_xor(qmax, 16, 64));
-  qmax = fmaxf(qmax, __shfl_xor(qmax, 32, 64));
-  const int e_q = exponent_of(qmax);
-  const float q_scale = ldexpf(1.0f, -e_q);
-  // Step st (0..7) covers dims d = 32kg + 4st + {0..3}; its 8 k-elements are
-  // [x(d0) x(d1) y(d0) y(d1) x(d2) x(d3) y(d2) y(d3)], matched on the key side by
-  // [hi(d0) hi(d1) lo(d0) lo(d1) hi(d2) hi(d3) lo(d2) lo(d3)] (two LUT pairs).
-  // x = q hi (columns < Q) or q lo (columns 8..8+Q), y = q hi (columns < Q), so
-  // column j + column 8+j = qh.kh + qh.kl + ql.kh.
-  if (w == 0) {
-#pragma unroll
-    for (int st = 0; st < 8; ++st) {
-      uint32_t xw[2], yw[2];
-#pragma unroll
-      for (int pr2 = 0; pr2 < 2; ++pr2) {
-        uint32_t xx = 0, yy = 0;
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          const float x = qv[4 * st + 2 * pr2 + hh] * q_scale;
-          const _Float16 hi = (_Float16)x;
-          const _Float16 lo = (_Float16)(x - (float)hi);
-          const uint32_t hb = f16_bits(hi), lb = f16_bits(lo);
-          xx |= (n < Q ? hb : (qrow >= 0 ? lb : 0u)) << (16 * hh);
-          yy |= (n < Q ? hb : 0u) << (16 * hh);
-        }
-        xw[pr2] = xx;
-        yw[pr2] = yy;
-      }
-      bqs[st][lane] = u32x4{xw[0], yw[0], xw[1], yw[1]};
-    }
-  }
-  // score factor of query row qq: scale * log2(e) * 2^(e_q + e_lut), taken
-  // from column qq (its hi column)
-  const float rfac = __shfl(p.scale * kLog2e * ldexpf(1.0f, e_q + e_lut), qq, 64);
-  __syncthreads();
-
-  // ---- split range
-  // (wave-uniform values are pinned to SGPRs so the tile loop's control flow
-  // and address arithmetic stay scalar)
-  const int64_t len = uniform64(p.hist_len ? min((int64_t)p.hist_len[b], (int64_t)p.max_hist_len) : p.max_hist_len);
-  const int64_t s0 = (int64_t)s * split_len;
-  const int64_t s1 = uniform64(min(len, s0 + split_len));
+  s0 = uniform64(s0);
+  s1 = uniform64(s1);
   const uint8_t* kbytes = (const uint8_t*)p.key_bytes;
   const uint8_t* vbytes = (const uint8_t*)p.val_bytes;
   const TN* norms = (const TN*)p.key_norms;
   const TV* vsc = (const TV*)p.val_scales;
   const TV* vzr = (const TV*)p.val_zeros;
 
-  // reference max / running sum of query row qq (max replicated over its 16
-  // lanes; the sum is this lane's share, reduced once at the end)
-  float m_run = -__builtin_inff(), l_run = 0.0f;
-  f32x4 acc_o[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) acc_o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  f32x4 acc_s = {0.f, 0.f, 0.f, 0.f};  // sum of A per row (query kg, group v)
-  float zacc[4] = {0.f, 0.f, 0.f, 0.f};  // this lane's share of sum p * zero, query qq
-  const u32x4 kOnesBf16 = u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
-  // bf16 128.0 in both halves, and the four 2-bit field masks of a spread
-  // code byte; hidden from constant folding so that each B operand dword is a
-  // single v_and_or_b32 (mask from an SGPR, base from a VGPR) rather than an
-  // and plus an or with two literals
-  uint32_t bf16_base = 0x43004300u;
-  asm volatile("" : "+v"(bf16_base));
-  uint32_t fmask[4] = {0x00030003u, 0x000c000cu, 0x00300030u, 0x00600060u};
-#pragma unroll
-  for (int f = 0; f < 4; ++f) asm volatile("" : "+s"(fmask[f]));
-
-  // LDS addresses (lane constants)
-  uint8_t* const vw = &vsp[w][kVRow * 4 * pq + 8 * tq];       // spread writer, code byte 4pq
-  const uint8_t* const vr = &vsp[w][kVRow * n + 16 * kg];     // B reader: byte n (+16 rows: 16+n)
-  uint8_t* const aw = &ast[w][kARow * 4 * qq + 4 * (tokA >> 1)];  // A writer: row (qq, group 0)
-  const uint8_t* const ar = &ast[w][kARow * n + 16 * kg];     // A reader: row n, tokens 8kg..
-
   // row of history token t0g (a multiple of 16): rows t0g .. t0g + 15 are
   // consecutive in both layouts (paged blocks hold a multiple of 16 tokens)
   const int64_t contig_base = uniform64(addr.table ? 0
-      : (int64_t)h * addr.head_stride + (addr.seq_start ? addr.seq_start[b] : (int64_t)b * addr.uniform_len));
+      : (int64_t)h * addr.head_stride + (addr.seq_start ? ((ConstI64Ptr)addr.seq_start)[b] : (int64_t)b * addr.uniform_len));
   // block table row of this sequence, read through the scalar cache
-  typedef const __attribute__((address_space(4))) int* ConstIntPtr;
   const bool paged = __builtin_amdgcn_readfirstlane(addr.table != nullptr ? 1 : 0) != 0;
   const ConstIntPtr tbl =
       (ConstIntPtr)uniform64(paged ? (int64_t)(uintptr_t)(addr.table + (int64_t)b * addr.max_blocks) : 0);
@@ -461,6 +423,156 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
       }
     }
   };
+
+  u32x4 kqa, kqb;
+  uint32_t vd[4];
+  NormPair<TN> nrm;
+  Pack8<TV> sv, zv;
+  auto none = [] {};
+  int64_t t0 = s0 + (int64_t)wu * kMTile;
+  // Pipelined loops over full tiles with even rows (paged rows always are;
+  // contiguous rows when the head's first row is even).  Each iteration
+  // issues the next tile's loads once this tile's registers are consumed, so
+  // every load has one iteration to arrive; the last iteration reloads its
+  // own rows (cache hits) to keep the load sequence identical.
+  const bool even_rows = paged || (contig_base & 1) == 0;
+  // Contiguous rows: the split's full 128-token steps (one 32-token tile per
+  // wave) in a rotated order whose start differs between workgroups.  Every
+  // split starts at the same offset of its sequence's arrays, so without the
+  // rotation concurrent workgroups stream the same address phase; measured on
+  // MI355X, the rotation alone takes the load stream from 5.6 to 5.9 TB/s.
+  // The next row is formed without a branch: with a branch at the loop top
+  // the compiler waits for every load of the tile there instead of for each
+  // array when it is first used.
+  const int64_t n_steps = (s1 - s0) / (kMWaves * kMTile);
+  constexpr int64_t kStep = kMWaves * kMTile;
+  const bool rot = !paged && even_rows && n_steps > 0;
+  const int K = __builtin_amdgcn_readfirstlane((int)(rot ? n_steps : 1));
+  const int r = __builtin_amdgcn_readfirstlane(
+      (int)(((unsigned)gx * 7u + (unsigned)gy * 13u + (unsigned)gz * 5u) % (unsigned)K));
+  const int64_t base = uniform64(contig_base + s0 + (int64_t)wu * kMTile);  // step 0 of this wave
+  const int64_t wrap = (int64_t)K * kStep;
+  const int64_t rot_end = base + wrap;
+  int64_t row = uniform64(base + (int64_t)r * kStep);
+  // The rotated loop's first tile is pulled into the caches here, ahead of
+  // the prologue's own work, so that its loads after the prologue hit L2
+  // instead of paying a full memory round trip: one dword per lane, every
+  // 128-byte line of the tile's five arrays touched by some lane (a point
+  // every 128 bytes from each array's first byte, the last at its last dword).
+  // Other paths read the query row instead: the load is issued on every path,
+  // because a load under a branch makes the compiler wait for every load
+  // where the paths join.
+  uint32_t warm;
+  {
+    constexpr int kKeyPts = 17, kValPts = 9, kNrmPts = 2;  // 2 KB, 1 KB, <= 128 B
+    constexpr int kSidePts = sizeof(TV) == 2 ? 3 : 5;      // 256 or 512 B each
+    constexpr int kBytesSide = 32 * 4 * (int)sizeof(TV);
+    const uint8_t* pt = (const uint8_t*)qsrc;
+    int k = lane;
+    auto point = [&](const void* arr, int bytes, int npts) {
+      if (k >= 0 && k < npts) pt = (const uint8_t*)arr + min(128 * k, bytes - 4);
+      k -= npts;
+    };
+    point(kbytes + row * 64, 32 * 64, kKeyPts);
+    point(vbytes + row * 32, 32 * 32, kValPts);
+    point(norms + row, 32 * (int)sizeof(TN), kNrmPts);
+    point(vsc + row * 4, kBytesSide, kSidePts);
+    point(vzr + row * 4, kBytesSide, kSidePts);
+    if (!rot) pt = (const uint8_t*)qsrc;
+    warm = *(const uint32_t*)pt;
+  }
+
+  // ---- key LUT: byte (c0 | c1 << KBITS) -> packed f16 hi / lo of both codes,
+  // centroids pre-scaled by 2^-e_lut so the largest has magnitude in [1, 2)
+  float cmax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < (1 << KBITS); ++i) cmax = fmaxf(cmax, fabsf(cent[i]));
+  const int e_lut = exponent_of(cmax);
+  const float lut_scale = ldexpf(1.0f, -e_lut);
+  {
+    const int v = tid;  // 256 threads, one entry each
+    float c0 = cent[0], c1 = cent[0];
+#pragma unroll
+    for (int i = 1; i < (1 << KBITS); ++i) {
+      c0 = (v & kMask) == (uint32_t)i ? cent[i] : c0;
+      c1 = ((v >> KBITS) & kMask) == (uint32_t)i ? cent[i] : c1;
+    }
+    c0 *= lut_scale;
+    c1 *= lut_scale;
+    const _Float16 h0 = (_Float16)c0, h1 = (_Float16)c1;
+    const _Float16 l0 = (_Float16)(c0 - (float)h0), l1 = (_Float16)(c1 - (float)h1);
+    lut[v] = u32x2{f16_bits(h0) | (f16_bits(h1) << 16), f16_bits(l0) | (f16_bits(l1) << 16)};
+  }
+
+  // ---- query B operands: columns [0, Q) hold the hi parts of query rows
+  // 0..Q-1, columns [8, 8+Q) their lo parts, the rest zero
+  float qmax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) qmax = fmaxf(qmax, fabsf(qv[i]));
+  qmax = fmaxf(qmax, __shfl_xor(qmax, 16, 64));
+  qmax = fmaxf(qmax, __shfl_xor(qmax, 32, 64));
+  const int e_q = exponent_of(qmax);
+  const float q_scale = ldexpf(1.0f, -e_q);
+  // Step st (0..7) covers dims d = 32kg + 4st + {0..3}; its 8 k-elements are
+  // [x(d0) x(d1) y(d0) y(d1) x(d2) x(d3) y(d2) y(d3)], matched on the key side by
+  // [hi(d0) hi(d1) lo(d0) lo(d1) hi(d2) hi(d3) lo(d2) lo(d3)] (two LUT pairs).
+  // x = q hi (columns < Q) or q lo (columns 8..8+Q), y = q hi (columns < Q), so
+  // column j + column 8+j = qh.kh + qh.kl + ql.kh.
+  if (w == 0) {
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+      uint32_t xw[2], yw[2];
+#pragma unroll
+      for (int pr2 = 0; pr2 < 2; ++pr2) {
+        uint32_t xx = 0, yy = 0;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const float x = qv[4 * st + 2 * pr2 + hh] * q_scale;
+          const _Float16 hi = (_Float16)x;
+          const _Float16 lo = (_Float16)(x - (float)hi);
+          const uint32_t hb = f16_bits(hi), lb = f16_bits(lo);
+          xx |= (n < Q ? hb : (qrow >= 0 ? lb : 0u)) << (16 * hh);
+          yy |= (n < Q ? hb : 0u) << (16 * hh);
+        }
+        xw[pr2] = xx;
+        yw[pr2] = yy;
+      }
+      bqs[st][lane] = u32x4{xw[0], yw[0], xw[1], yw[1]};
+    }
+  }
+  // score factor of query row qq: scale * log2(e) * 2^(e_q + e_lut), taken
+  // from column qq (its hi column)
+  const float rfac = __shfl(p.scale * kLog2e * ldexpf(1.0f, e_q + e_lut), qq, 64);
+  // LDS-only barrier: the first tile's global loads stay in flight
+  __builtin_amdgcn_s_waitcnt(kWaitLdsOnly);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+
+  // reference max / running sum of query row qq (max replicated over its 16
+  // lanes; the sum is this lane's share, reduced once at the end)
+  float m_run = -__builtin_inff(), l_run = 0.0f;
+  f32x4 acc_o[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc_o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 acc_s = {0.f, 0.f, 0.f, 0.f};  // sum of A per row (query kg, group v)
+  float zacc[4] = {0.f, 0.f, 0.f, 0.f};  // this lane's share of sum p * zero, query qq
+  const u32x4 kOnesBf16 = u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+  // bf16 128.0 in both halves, and the four 2-bit field masks of a spread
+  // code byte; hidden from constant folding so that each B operand dword is a
+  // single v_and_or_b32 (mask from an SGPR, base from a VGPR) rather than an
+  // and plus an or with two literals
+  uint32_t bf16_base = 0x43004300u;
+  asm volatile("" : "+v"(bf16_base));
+  uint32_t fmask[4] = {0x00030003u, 0x000c000cu, 0x00300030u, 0x00600060u};
+#pragma unroll
+  for (int f = 0; f < 4; ++f) asm volatile("" : "+s"(fmask[f]));
+
+  // LDS addresses (lane constants)
+  uint8_t* const vw = &vsp[w][kVRow * 4 * pq + 8 * tq];       // spread writer, code byte 4pq
+  const uint8_t* const vr = &vsp[w][kVRow * n + 16 * kg];     // B reader: byte n (+16 rows: 16+n)
+  uint8_t* const aw = &ast[w][kARow * 4 * qq + 4 * (tokA >> 1)];  // A writer: row (qq, group 0)
+  const uint8_t* const ar = &ast[w][kARow * n + 16 * kg];     // A reader: row n, tokens 8kg..
 
   float m_thr = -__builtin_inff();  // m_run + kLazyRescale
   // One tile.  The hooks run right after the tile's copy of the matching
@@ -604,41 +716,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
     wave_sync();  // this tile's LDS reads complete before the next tile's writes
   };
 
-  u32x4 kqa, kqb;
-  uint32_t vd[4];
-  NormPair<TN> nrm;
-  Pack8<TV> sv, zv;
-  auto none = [] {};
-  int64_t t0 = s0 + (int64_t)wu * kMTile;
-  // Pipelined loops over full tiles with even rows (paged rows always are;
-  // contiguous rows when the head's first row is even).  Each iteration
-  // issues the next tile's loads once this tile's registers are consumed, so
-  // every load has one iteration to arrive; the last iteration reloads its
-  // own rows (cache hits) to keep the load sequence identical.
-  const bool even_rows = paged || (contig_base & 1) == 0;
-  // Contiguous rows: the split's full 128-token steps (one 32-token tile per
-  // wave) in a rotated order whose start differs between workgroups.  Every
-  // split starts at the same offset of its sequence's arrays, so without the
-  // rotation concurrent workgroups stream the same address phase; measured on
-  // MI355X, the rotation alone takes the load stream from 5.6 to 5.9 TB/s.
-  // The next row is formed without a branch: with a branch at the loop top
-  // the compiler waits for every load of the tile there instead of for each
-  // array when it is first used.
-  const int64_t n_steps = (s1 - s0) / (kMWaves * kMTile);
-  if (!paged && even_rows && n_steps > 0) {
-    constexpr int64_t kStep = kMWaves * kMTile;
-    const int K = __builtin_amdgcn_readfirstlane((int)n_steps);
-    const int r = __builtin_amdgcn_readfirstlane(
-        (int)((blockIdx.x * 7u + blockIdx.y * 13u + blockIdx.z * 5u) % (unsigned)K));
-    const int64_t base = uniform64(contig_base + s0 + (int64_t)wu * kMTile);  // step 0 of this wave
-    const int64_t wrap = (int64_t)K * kStep;
-    const int64_t rot_end = base + wrap;
-    int64_t row = uniform64(base + (int64_t)r * kStep);
+  if (rot) {
     const TileDesc dc{row, row + 16, 31};
     fast_values(dc, vd);
     fast_keys(dc, kqa, kqb);
     fast_norms(dc, nrm);
     fast_side(dc, sv, zv);
+    asm volatile("" ::"v"(warm));  // keeps the warm-up load (done by now)
     for (int i = 0;;) {
       ++i;
       const bool more = i < K;
@@ -756,21 +840,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
     red_l[w][lane] = l_run;
   }
   __syncthreads();
-  // ---- merge the 4 waves into this split's partial (natural-log units)
-  for (int i = tid; i < Q * 128; i += 256) {
-    const int j = i >> 7, d = i & 127;
-    float M = -__builtin_inff();
-    for (int ww = 0; ww < kMWaves; ++ww)
-      if (red_l[ww][j] > 0.0f) M = fmaxf(M, red_m[ww][j]);
-    float L = 0.0f, O = 0.0f;
+  // ---- merge the 4 waves into this split's partial (natural-log units).
+  // Each thread takes two adjacent dims of one query row and reads all its
+  // LDS operands before using any (waves without tokens, l = 0, are skipped).
+  for (int i = tid; i < Q * 64; i += 256) {
+    const int j = i >> 6, d = 2 * (i & 63);
+    float mw[kMWaves], lw[kMWaves];
+    f32x2 ow[kMWaves];
+#pragma unroll
     for (int ww = 0; ww < kMWaves; ++ww) {
-      if (!(red_l[ww][j] > 0.0f)) continue;
-      const float f = exp2f(red_m[ww][j] - M);
-      L = fmaf(red_l[ww][j], f, L);
-      O = fmaf(red_o[ww][j][d], f, O);
+      mw[ww] = red_m[ww][j];
+      lw[ww] = red_l[ww][j];
+      ow[ww] = *(const f32x2*)&red_o[ww][j][d];
+    }
+    float M = -__builtin_inff();
+#pragma unroll
+    for (int ww = 0; ww < kMWaves; ++ww) M = lw[ww] > 0.0f ? fmaxf(M, mw[ww]) : M;
+    float L = 0.0f;
+    f32x2 O = {0.0f, 0.0f};
+#pragma unroll
+    for (int ww = 0; ww < kMWaves; ++ww) {
+      const bool live = lw[ww] > 0.0f;
+      const float f = live ? exp2f(mw[ww] - M) : 0.0f;
+      L = live ? fmaf(lw[ww], f, L) : L;
+      O[0] = live ? fmaf(ow[ww][0], f, O[0]) : O[0];
+      O[1] = live ? fmaf(ow[ww][1], f, O[1]) : O[1];
     }
     const int64_t pi = part.idx(b, h, p.n_kv_heads, Q, j, s);
-    part.o[pi * 128 + d] = O;
+    *(f32x2*)&part.o[pi * 128 + d] = O;
     if (d == 0) {
       part.m[pi] = M == -__builtin_inff() ? M : M * 0.6931471805599453f;
       part.l[pi] = L;
@@ -801,7 +898,7 @@ __global__ __launch_bounds__(kOrderBuckets) void decode_order_kernel(const long 
                                                                      long long max_len, int batch,
                                                                      int* __restrict__ order) {
   __shared__ int count[kOrderBuckets];
-  const int tid = threadIdx.x;
+  const int tid = (int)__builtin_amdgcn_workitem_id_x();
   count[tid] = 0;
   __syncthreads();
   auto bucket = [&](int b) {
@@ -835,7 +932,8 @@ int launch_decode_order(const smaq_attn_params& p, int* order, hipStream_t st) {
 // workgroup slots (kDecodeWaves workgroups of 4 waves per CU): a workgroup's
 // fixed costs (its prologue and first tile's latency, the 4-wave merge) are
 // then paid once per slot (c3: 4 splits, 1024 workgroups, 0.177 ms against
-// 0.183 ms for two rounds of half the length).
+// 0.183 ms for two rounds of half the length).  The length returned sets the
+// number of splits; the kernel places the boundaries (SplitRule).
 int64_t mfma_decode_split_len(const smaq_attn_params& p) {
   const int64_t units = (int64_t)p.batch * p.n_kv_heads;
   const bool wide = p.norm_dtype == SMAQ_F32 || p.val_dtype == SMAQ_F32;
@@ -847,39 +945,54 @@ int64_t mfma_decode_split_len(const smaq_attn_params& p) {
   return split < 4 * q ? 4 * q : split;
 }
 
+// Weight step per round-slot with 4 slots per CU: splits weigh 64, 54, 44, 34
+// (c3 on MI355X, kernel alone: 0.1791-0.1809 ms against 0.1825-0.1841 ms for
+// equal splits; steps of 8 and 12 measured between, 14 and above slower).
+// With 3 slots (fp32 metadata) the splits stay equal (not measured).
+constexpr int kSplitTilt4 = 10;
+static_assert(kSplitTilt4 * 3 < kSplitWeight, "split weights must stay positive");
+
 template <int KB, typename TN, bool SPLIT>
-static void launch_v(const smaq_attn_params& p, const HistAddr& a, const Partials& part,
-                     int64_t split_len, int n_splits, const int* order, hipStream_t st) {
-  dim3 grid(n_splits, p.n_kv_heads, p.batch);
+static void launch_v(const smaq_attn_params& p, const HistAddr& a, const Partials& part, const SplitRule& rule,
+                     int n_splits, const int* order, hipStream_t st) {
+  // heads fastest, then sequences (the longest-first order when given), then
+  // splits: split-major, so that a one-round grid runs split s in round-slot s
+  dim3 grid(p.n_kv_heads, p.batch, n_splits);
   switch (p.val_dtype) {
-    case SMAQ_F32: hipLaunchKernelGGL((decode_mfma_kernel<KB, TN, float, SPLIT>), grid, dim3(256), 0, st, p, a, part, split_len, order); break;
-    case SMAQ_F16: hipLaunchKernelGGL((decode_mfma_kernel<KB, TN, _Float16, SPLIT>), grid, dim3(256), 0, st, p, a, part, split_len, order); break;
-    default: hipLaunchKernelGGL((decode_mfma_kernel<KB, TN, bf16, SPLIT>), grid, dim3(256), 0, st, p, a, part, split_len, order); break;
+    case SMAQ_F32: hipLaunchKernelGGL((decode_mfma_kernel<KB, TN, float, SPLIT>), grid, dim3(256), 0, st, p, a, part, rule, order); break;
+    case SMAQ_F16: hipLaunchKernelGGL((decode_mfma_kernel<KB, TN, _Float16, SPLIT>), grid, dim3(256), 0, st, p, a, part, rule, order); break;
+    default: hipLaunchKernelGGL((decode_mfma_kernel<KB, TN, bf16, SPLIT>), grid, dim3(256), 0, st, p, a, part, rule, order); break;
   }
 }
 
 template <int KB, typename TN>
-static void launch_s(const smaq_attn_params& p, const HistAddr& a, const Partials& part,
-                     int64_t split_len, int n_splits, const int* order, hipStream_t st) {
+static void launch_s(const smaq_attn_params& p, const HistAddr& a, const Partials& part, const SplitRule& rule,
+                     int n_splits, const int* order, hipStream_t st) {
   // 16-token pages put a tile's two 16-token groups in different blocks
-  if (p.block_table && p.block_size == 16) launch_v<KB, TN, true>(p, a, part, split_len, n_splits, order, st);
-  else launch_v<KB, TN, false>(p, a, part, split_len, n_splits, order, st);
+  if (p.block_table && p.block_size == 16) launch_v<KB, TN, true>(p, a, part, rule, n_splits, order, st);
+  else launch_v<KB, TN, false>(p, a, part, rule, n_splits, order, st);
 }
 
 template <int KB>
-static void launch_n(const smaq_attn_params& p, const HistAddr& a, const Partials& part,
-                     int64_t split_len, int n_splits, const int* order, hipStream_t st) {
+static void launch_n(const smaq_attn_params& p, const HistAddr& a, const Partials& part, const SplitRule& rule,
+                     int n_splits, const int* order, hipStream_t st) {
   switch (p.norm_dtype) {
-    case SMAQ_F32: launch_s<KB, float>(p, a, part, split_len, n_splits, order, st); break;
-    case SMAQ_F16: launch_s<KB, _Float16>(p, a, part, split_len, n_splits, order, st); break;
-    default: launch_s<KB, bf16>(p, a, part, split_len, n_splits, order, st); break;
+    case SMAQ_F32: launch_s<KB, float>(p, a, part, rule, n_splits, order, st); break;
+    case SMAQ_F16: launch_s<KB, _Float16>(p, a, part, rule, n_splits, order, st); break;
+    default: launch_s<KB, bf16>(p, a, part, rule, n_splits, order, st); break;
   }
 }
 
 int launch_mfma_decode(const smaq_attn_params& p, const HistAddr& a, const Partials& part,
-                       int64_t split_len, int n_splits, const int* order, hipStream_t st) {
-  if (p.key_bits == 3) launch_n<3>(p, a, part, split_len, n_splits, order, st);
-  else launch_n<4>(p, a, part, split_len, n_splits, order, st);
+                       int64_t /*split_len*/, int n_splits, const int* order, hipStream_t st) {
+  const bool wide = p.norm_dtype == SMAQ_F32 || p.val_dtype == SMAQ_F32;
+  SplitRule rule;
+  rule.n_splits = n_splits;
+  rule.n_cu = device_cu_count();
+  rule.slots = wide ? 3 : 4;
+  rule.tilt = wide ? 0 : kSplitTilt4;
+  if (p.key_bits == 3) launch_n<3>(p, a, part, rule, n_splits, order, st);
+  else launch_n<4>(p, a, part, rule, n_splits, order, st);
   return launch_status("smaq_attn_hybrid(mfma decode)");
 }
 

@@ -65,24 +65,35 @@ constexpr int kWaitLdsOnly = 0xC07F;
 // 169 us.  Split s therefore weighs kSplitWeight - tilt * k, and its first
 // token is the sequence length times the weight of the splits before it over
 // the total, rounded down to whole 128-token steps.
+constexpr int kMaxSlots = 4;
 struct SplitRule {
   int n_splits;
   int n_cu;   // workgroups per round-slot (the device's CU count)
-  int slots;  // round-slots per CU
+  int slots;  // round-slots per CU (at most kMaxSlots)
   int tilt;   // weight step per slot; tilt * (slots - 1) < kSplitWeight
 };
 constexpr int kSplitWeight = 64;
 
-// Weight of splits 0 .. s-1 of unit u (of `units`).
-__device__ __forceinline__ int split_weight_before(const SplitRule& r, int u, int units, int s) {
-  int c = kSplitWeight * s;
-  for (int j = 1; j < r.slots; ++j) {
-    const int num = j * r.n_cu - u;  // splits >= first run in slot j or later
-    const int first = num <= 0 ? 0 : (int)(((unsigned)num + (unsigned)units - 1u) / (unsigned)units);
-    c -= r.tilt * (s > first ? s - first : 0);
+// The splits of unit u (of `units`) from which on the round-slot is at
+// least j, for j = 1 .. slots-1.
+struct SlotStarts {
+  int first[kMaxSlots];
+  __device__ __forceinline__ SlotStarts(const SplitRule& r, int u, int units) {
+#pragma unroll
+    for (int j = 1; j < kMaxSlots; ++j) {
+      const int num = j * r.n_cu - u;
+      first[j] = j >= r.slots ? 0x7fffffff
+                              : (num <= 0 ? 0 : (int)(((unsigned)num + (unsigned)units - 1u) / (unsigned)units));
+    }
   }
-  return c;
-}
+  // weight of splits 0 .. s-1
+  __device__ __forceinline__ int weight_before(const SplitRule& r, int s) const {
+    int c = kSplitWeight * s;
+#pragma unroll
+    for (int j = 1; j < kMaxSlots; ++j) c -= r.tilt * (s > first[j] ? s - first[j] : 0);
+    return c;
+  }
+};
 
 // Rows of one 32-token tile: tokens 0..15 at rows gA.., 16..31 at gB..
 struct TileDesc {
@@ -300,6 +311,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
     const float4 v4 = *(const float4*)(qsrc + 32 * kg + i);
     qv[i] = v4.x; qv[i + 1] = v4.y; qv[i + 2] = v4.z; qv[i + 3] = v4.w;
   }
+  // (nothing below is scheduled above the query loads: they need only the
+  // query pointer and the head counts, and go out before the other argument
+  // reads and their waits)
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int i = 0; i < 32; ++i) qv[i] = qrow < 0 ? 0.0f : qv[i];
   float cent[1 << KBITS];
@@ -318,10 +333,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
     // (a shared boundary is computed by the same expression for both of its
     // splits, so rounding cannot open a gap or an overlap)
     const int units = p.n_kv_heads * p.batch, u = h + p.n_kv_heads * gy;
-    const double per_weight = (double)len / (double)split_weight_before(rule, u, units, rule.n_splits);
+    const SlotStarts starts(rule, u, units);
+    const double per_weight = (double)len / (double)starts.weight_before(rule, rule.n_splits);
     constexpr int64_t kStepMask = ~(int64_t)(kMWaves * kMTile - 1);
-    if (s > 0) s0 = (int64_t)(per_weight * split_weight_before(rule, u, units, s)) & kStepMask;
-    if (s + 1 < rule.n_splits) s1 = (int64_t)(per_weight * split_weight_before(rule, u, units, s + 1)) & kStepMask;
+    if (s > 0) s0 = (int64_t)(per_weight * starts.weight_before(rule, s)) & kStepMask;
+    if (s + 1 < rule.n_splits) s1 = (int64_t)(per_weight * starts.weight_before(rule, s + 1)) & kStepMask;
   }
   s0 = uniform64(s0);
   s1 = uniform64(s1);

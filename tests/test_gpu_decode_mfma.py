@@ -53,8 +53,9 @@ def test_mfma_decode_contiguous(dev, bits, g, dtype):
 
 def test_mfma_decode_many_splits(dev):
     """One sequence, 2 KV heads, 20000 tokens: the context is cut into 40
-    splits of 512 tokens, so the split merge runs five chunks of loads and
-    rescales its sums whenever a later chunk holds a larger maximum."""
+    splits of 384-512 tokens (whole 128-token steps), so the split merge runs
+    five chunks of loads and rescales its sums whenever a later chunk holds a
+    larger maximum."""
     strat, codec = _codec_pair(dev, 3, 280)
     hkv, g, n = 2, 4, 20000
     keys = sample_keys(n * hkv, seed=281).reshape(n, hkv, 128).bfloat16()
@@ -65,6 +66,25 @@ def test_mfma_decode_many_splits(dev):
     q = keys[18000].float().repeat_interleave(g, dim=0).unsqueeze(0).bfloat16()
     out = kvb.attention(q.to(dev), impl=2)
     assert_attn_close(out, _oracle(codec, keys, vals, q, hkv * g, hkv), "mfma 40 splits")
+
+
+def test_mfma_decode_slot_weighted_splits(dev):
+    """8 ragged sequences x 8 KV heads = 64 units: a one-round grid of 16
+    splits per unit spans four round-slots per CU, so the splits of later
+    slots are shorter (weights 64 - 10 * slot) and every boundary falls on a
+    whole 128-token step of each sequence's own length."""
+    strat, codec = _codec_pair(dev, 3, 300)
+    hkv, g = 8, 4
+    lens = [3001, 8192, 4500, 129, 7777, 5000, 2048, 6100]
+    gen = torch.Generator().manual_seed(301)
+    keys = [sample_keys(n * hkv, seed=310 + i).reshape(n, hkv, 128).bfloat16() for i, n in enumerate(lens)]
+    vals = [torch.randn(n, hkv, 128, generator=gen).bfloat16() for n in lens]
+    kvb = QuantizedKVBatch.encode(strat, [k.to(dev) for k in keys], [v.to(dev) for v in vals])
+    q = torch.randn(len(lens), hkv * g, 128, generator=gen).bfloat16()
+    out = kvb.attention(q.to(dev), impl=2)
+    for b in (0, 1, 3, 4, 7):
+        ref = _oracle(codec, keys[b], vals[b], q[b:b + 1], hkv * g, hkv)
+        assert_attn_close(out[b:b + 1], ref, f"slot-weighted splits seq {b} len {lens[b]}")
 
 
 def test_mfma_decode_paged(dev):

@@ -59,12 +59,11 @@ constexpr int kWaitLdsOnly = 0xC07F;
 // Split boundaries.  The grid (KV heads, sequences, splits) is dispatched
 // split-major, so with one round of workgroups, split s of unit u = head +
 // n_kv_heads * sequence runs in round-slot k = (u + units * s) / n_cu of its
-// CU.  A CU's
-// memory pipeline serves its earlier-dispatched workgroups first: with equal
-// splits (c3 on MI355X, 4 slots per CU) the slots took 147, 154, 162 and
-// 169 us.  Split s therefore weighs kSplitWeight - tilt * k, and its first
-// token is the sequence length times the weight of the splits before it over
-// the total, rounded down to whole 128-token steps.
+// CU.  A CU's memory pipeline serves its earlier-dispatched workgroups first:
+// with equal splits (c3 on MI355X, 4 slots per CU) the slots took 147, 154,
+// 162 and 169 us.  Split s therefore weighs kSplitWeight - tilt * k, and its
+// first token is the sequence length times the weight of the splits before it
+// over the total, rounded down to whole 128-token steps.
 constexpr int kMaxSlots = 4;
 struct SplitRule {
   int n_splits;

@@ -531,6 +531,9 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
   part.o = part.l + n_part;
 
   const int phases = p.phases ? p.phases : 7;
+  // The matrix-core decode kernel writes the output itself when the history
+  // is one split and there is no recent part: no combine launch.
+  const bool direct = pl.mfma && pl.s_hist == 1 && pl.s_recent == 0;
   if (pl.prefill) {
     char* ws = (char*)p.workspace + align256(n_part * (p.head_dim + 2) * (int64_t)sizeof(float));
     auto planes = [&](int64_t lp) {
@@ -569,7 +572,7 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
         order = (int*)((char*)p.workspace + align256(partial_bytes(&p, pl)));
         if ((rc = launch_decode_order(p, order, st)) != SMAQ_OK) return rc;
       }
-      rc = launch_mfma_decode(p, a, part, pl.hist_split, pl.s_hist, order, st);
+      rc = launch_mfma_decode(p, a, part, pl.s_hist, direct, order, st);
       if (rc != SMAQ_OK) return rc;
     } else if (p.key_format == SMAQ_KEY_SCALAR) {
       switch (p.norm_dtype) {
@@ -595,7 +598,7 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
     const int rc = launch_status("smaq_attn_hybrid(recent)");
     if (rc != SMAQ_OK) return rc;
   }
-  if (!(phases & 4)) return SMAQ_OK;
+  if (!(phases & 4) || direct) return SMAQ_OK;
   dim3 cgrid((unsigned)((rows + kCombineRows - 1) / kCombineRows), p.n_kv_heads, p.batch);
   const dim3 cblock((unsigned)((p.head_dim + 63) / 64 * 64), kCombineRows);  // one thread per output dim
   switch (p.out_dtype) {

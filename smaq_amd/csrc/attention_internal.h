@@ -73,7 +73,9 @@ int64_t mfma_decode_split_len(const smaq_attn_params& p);
 // order their workgroups are dispatched; launch_decode_order fills it with
 // the sequences by history length, longest first.
 int launch_decode_order(const smaq_attn_params& p, int* order, hipStream_t st);
+// With `direct` (one split and no recent part) the kernel writes the final
+// output itself, and no split combine is needed.
 int launch_mfma_decode(const smaq_attn_params& p, const HistAddr& a, const Partials& part,
-                       int64_t split_len, int n_splits, const int* order, hipStream_t st);
+                       int n_splits, bool direct, const int* order, hipStream_t st);
 
 }  // namespace smaq

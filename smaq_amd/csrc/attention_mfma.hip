@@ -70,6 +70,7 @@ struct SplitRule {
   int n_cu;   // workgroups per round-slot (the device's CU count)
   int slots;  // round-slots per CU (at most kMaxSlots)
   int tilt;   // weight step per slot; tilt * (slots - 1) < kSplitWeight
+  int direct; // one split and no recent part: write the final output
 };
 constexpr int kSplitWeight = 64;
 
@@ -881,11 +882,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
       O[0] = live ? fmaf(ow[ww][0], f, O[0]) : O[0];
       O[1] = live ? fmaf(ow[ww][1], f, O[1]) : O[1];
     }
-    const int64_t pi = part.idx(b, h, p.n_kv_heads, Q, j, s);
-    *(f32x2*)&part.o[pi * 128 + d] = O;
-    if (d == 0) {
-      part.m[pi] = M == -__builtin_inff() ? M : M * 0.6931471805599453f;
-      part.l[pi] = L;
+    if (rule.direct) {
+      // the output itself: the split combine's arithmetic for one partial
+      // (o * (1 / l), zero without tokens), in the output dtype
+      const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+      const float r0 = O[0] * inv, r1 = O[1] * inv;
+      const int64_t oi = ((int64_t)b * p.n_q_heads + h * Q + j) * 128 + d;
+      switch (p.out_dtype) {
+        case SMAQ_F32: {
+          float* o = (float*)p.out + oi;
+          o[0] = r0;
+          o[1] = r1;
+        } break;
+        case SMAQ_F16: {
+          _Float16* o = (_Float16*)p.out + oi;
+          o[0] = Num<_Float16>::from_f(r0);
+          o[1] = Num<_Float16>::from_f(r1);
+        } break;
+        default: {
+          bf16* o = (bf16*)p.out + oi;
+          o[0] = Num<bf16>::from_f(r0);
+          o[1] = Num<bf16>::from_f(r1);
+        } break;
+      }
+    } else {
+      const int64_t pi = part.idx(b, h, p.n_kv_heads, Q, j, s);
+      *(f32x2*)&part.o[pi * 128 + d] = O;
+      if (d == 0) {
+        part.m[pi] = M == -__builtin_inff() ? M : M * 0.6931471805599453f;
+        part.l[pi] = L;
+      }
     }
   }
 }
@@ -999,13 +1025,14 @@ static void launch_n(const smaq_attn_params& p, const HistAddr& a, const Partial
 }
 
 int launch_mfma_decode(const smaq_attn_params& p, const HistAddr& a, const Partials& part,
-                       int64_t /*split_len*/, int n_splits, const int* order, hipStream_t st) {
+                       int n_splits, bool direct, const int* order, hipStream_t st) {
   const bool wide = p.norm_dtype == SMAQ_F32 || p.val_dtype == SMAQ_F32;
   SplitRule rule;
   rule.n_splits = n_splits;
   rule.n_cu = device_cu_count();
   rule.slots = wide ? 3 : 4;
   rule.tilt = wide ? 0 : kSplitTilt4;
+  rule.direct = direct && n_splits == 1 ? 1 : 0;
   if (p.key_bits == 3) launch_n<3>(p, a, part, rule, n_splits, order, st);
   else launch_n<4>(p, a, part, rule, n_splits, order, st);
   return launch_status("smaq_attn_hybrid(mfma decode)");

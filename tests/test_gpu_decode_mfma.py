@@ -87,6 +87,35 @@ def test_mfma_decode_slot_weighted_splits(dev):
         assert_attn_close(out[b:b + 1], ref, f"slot-weighted splits seq {b} len {lens[b]}")
 
 
+@pytest.mark.parametrize("qdtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_mfma_decode_direct_output(dev, qdtype):
+    """Contexts of at most 512 tokens give one split per (sequence, head) and
+    no recent part, so the decode kernel writes the output itself (no split
+    combine); a history phase followed by a separate combine phase gives the
+    same bits."""
+    strat, codec = _codec_pair(dev, 3, 320)
+    hkv, g = 8, 4
+    lens = [300, 512, 17, 200, 64]
+    gen = torch.Generator().manual_seed(321)
+    keys = [sample_keys(n * hkv, seed=330 + i).reshape(n, hkv, 128).bfloat16() for i, n in enumerate(lens)]
+    vals = [torch.randn(n, hkv, 128, generator=gen).bfloat16() for n in lens]
+    kvb = QuantizedKVBatch.encode(strat, [k.to(dev) for k in keys], [v.to(dev) for v in vals])
+    q = torch.randn(len(lens), hkv * g, 128, generator=gen).to(qdtype)
+    out = kvb.attention(q.to(dev), impl=2)
+    assert out.dtype == qdtype
+    for b in range(len(lens)):
+        ref = _oracle(codec, keys[b], vals[b], q[b:b + 1], hkv * g, hkv)
+        assert_attn_close(out[b:b + 1], ref, f"direct output {qdtype} seq {b} len {lens[b]}")
+    plan = kvb.plan(q.to(dev))
+    full = plan.run(q.to(dev)).clone()
+    plan.out.zero_()
+    plan.load_query(q.to(dev))
+    plan.launch(phases=1)
+    plan.launch(phases=4)
+    torch.cuda.synchronize()
+    assert torch.equal(plan.out, full)
+
+
 def test_mfma_decode_paged(dev):
     strat, codec = _codec_pair(dev, 3, 260)
     gen = torch.Generator().manual_seed(261)

@@ -232,7 +232,9 @@ typedef struct smaq_attn_params {
   /* 0 = run everything; else a bit mask of phases to launch, so a caller can
      time them apart: 1 = history partials, 2 = recent partials, 4 = combine.
      Phases communicate through the workspace, launched in order on one
-     stream. */
+     stream.  When the matrix-core decode kernel serves the history as one
+     split per (sequence, KV head) and there is no recent part, phase 1
+     writes the output itself and phase 4 launches nothing. */
   int phases;
   /* kernel choice: 0 = automatic (matrix-core decode kernel when the shape
      allows, generic kernels otherwise), 1 = generic kernels only, 2 = the

@@ -987,9 +987,10 @@ int64_t mfma_decode_split_len(const smaq_attn_params& p) {
 }
 
 // Weight step per round-slot with 4 slots per CU: splits weigh 64, 54, 44, 34
-// (c3 on MI355X, kernel alone: 0.1791-0.1809 ms against 0.1825-0.1841 ms for
-// equal splits; steps of 8 and 12 measured between, 14 and above slower).
-// With 3 slots (fp32 metadata) the splits stay equal (not measured).
+// (c3 on MI355X, kernel alone, three alternating rounds on one box: steps
+// of 6 / 8 / 10 / 12 took 173.9 / 172.3 / 171.1 / 173.0 us; equal splits
+// were 2-3% slower than a step of 10 on other boxes, 14 and above slower
+// still).  With 3 slots (fp32 metadata) the splits stay equal (not measured).
 constexpr int kSplitTilt4 = 10;
 static_assert(kSplitTilt4 * 3 < kSplitWeight, "split weights must stay positive");
 

@@ -289,12 +289,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
   // this lane's two softmax tokens: C-layout values 2*bank, 2*bank + 1
   const int tokA = bank < 2 ? 4 * kg + 2 * bank : 16 + 4 * kg + 2 * (bank - 2);
   const int tq = lane & 7, pq = lane >> 3;           // value loader: tokens 4tq.., bytes 4pq..
-  const int s = gz, h = gx;
+  const int s = gz;
   // per-sequence lookups go through the scalar cache (no vector-memory wait
   // in the prologue)
   typedef const __attribute__((address_space(4))) int* ConstIntPtr;
   typedef const __attribute__((address_space(4))) int64_t* ConstI64Ptr;
-  const int b = order ? ((ConstIntPtr)order)[gy] : gy;
+  // Longest-first dispatch (one split per unit): the KV heads of a sequence
+  // share cache lines of the pools (a 16-token page's norms, scales and
+  // zeros are runs shorter than a line, next to the other heads' runs), and
+  // workgroup f runs on XCD f mod 8.  So each group of 8 sequences (in
+  // dispatch order) takes 8 * Hkv consecutive workgroups f = base + 8 h + i,
+  // which puts every head of sequence i on one XCD and its shared lines in
+  // one L2 (c5: HBM traffic +6.0% -> +0.8% over the algorithmic bytes).
+  int hsel = gx, osel = gy;
+  if (order) {
+    const int hk = p.n_kv_heads;
+    const int f = gx + hk * gy;
+    if (f < (p.batch / 8) * 8 * hk) {
+      const int grp = f / (8 * hk), rem = f - grp * 8 * hk;
+      hsel = rem >> 3;
+      osel = 8 * grp + (rem & 7);
+    }
+  }
+  const int h = __builtin_amdgcn_readfirstlane(hsel);
+  const int b = order ? ((ConstIntPtr)order)[__builtin_amdgcn_readfirstlane(osel)] : gy;
   const int Q = p.n_q_heads / p.n_kv_heads;  // query rows (decode: one token)
   constexpr uint32_t kMask = (1u << KBITS) - 1u;
   constexpr float kLog2e = 1.4426950408889634f;

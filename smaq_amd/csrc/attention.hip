@@ -448,9 +448,9 @@ extern "C" long long smaq_attn_workspace_bytes(const smaq_attn_params* p) {
   int64_t bytes = partial_bytes(p, pl);
   if (pl.longest_first) bytes = align256(bytes) + (int64_t)p->batch * (int64_t)sizeof(int);
   if (pl.prefill) {
-    // kPrefillPlanes f16 planes (key hi, key lo, values) per part
-    const int64_t per_tok = (int64_t)p->batch * p->n_kv_heads * p->head_dim * kPrefillPlanes * 2;
-    bytes = align256(bytes) + align256(pl.hist_lp * per_tok) + align256(pl.recent_lp * per_tok);
+    // tile images, value-lo planes and tile errors of each part
+    bytes = align256(bytes) + prefill_planes_bytes(p->batch, p->n_kv_heads, pl.hist_lp) +
+            prefill_planes_bytes(p->batch, p->n_kv_heads, pl.recent_lp);
   }
   return bytes;
 }
@@ -537,11 +537,8 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
   if (pl.prefill) {
     char* ws = (char*)p.workspace + align256(n_part * (p.head_dim + 2) * (int64_t)sizeof(float));
     auto planes = [&](int64_t lp) {
-      const int64_t n_el = (int64_t)p.batch * p.n_kv_heads * p.head_dim * lp;
-      PrefillPlanes P;
-      P.img = (_Float16*)ws;
-      P.Lp = lp;
-      ws += align256(n_el * kPrefillPlanes * 2);
+      const PrefillPlanes P = prefill_planes_at(ws, p.batch, p.n_kv_heads, lp);
+      ws += prefill_planes_bytes(p.batch, p.n_kv_heads, lp);
       return P;
     };
     const PrefillPlanes hp = planes(pl.hist_lp);
@@ -551,14 +548,14 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
                  p.block_size, p.n_kv_heads};
       int rc = launch_prefill_planes_hist(p, a, hp, st);
       if (rc != SMAQ_OK) return rc;
-      const PrefillPart pp{p.q_hist, hp.img, p.hist_len, p.max_hist_len, hp.Lp, pl.hist_split,
+      const PrefillPart pp{p.q_hist, hp.img, hp.img_lo, hp.err, p.hist_len, p.max_hist_len, hp.Lp, pl.hist_split,
                            p.hist_pos_offset, 0};
       if ((rc = launch_prefill_mfma(p, pp, pl.s_hist, part, st)) != SMAQ_OK) return rc;
     }
     if (pl.s_recent > 0 && (phases & 2)) {
       int rc = launch_prefill_planes_recent(p, rp, st);
       if (rc != SMAQ_OK) return rc;
-      const PrefillPart pp{p.q_exact, rp.img, p.recent_len, p.max_recent_len, rp.Lp, pl.recent_split,
+      const PrefillPart pp{p.q_exact, rp.img, rp.img_lo, rp.err, p.recent_len, p.max_recent_len, rp.Lp, pl.recent_split,
                            p.recent_pos_offset, pl.s_hist};
       if ((rc = launch_prefill_mfma(p, pp, pl.s_recent, part, st)) != SMAQ_OK) return rc;
     }

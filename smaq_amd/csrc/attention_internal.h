@@ -35,18 +35,29 @@ struct Partials {
 // Matrix-core prefill path (attention_prefill.hip).  Each attended part
 // (history, recent window) is first decoded into f16 tile images:
 // [B][Hkv][Lp / 64] tiles of 48 KB, each the LDS image the kernel copies
-// (key hi, key lo, values: kPrefillPlanes f16 planes of head_dim x 64;
-// layout in attention_prefill.hip).
+// (key hi, key lo, value hi: kPrefillPlanes f16 planes of head_dim x 64;
+// layout in attention_prefill.hip), a 16 KB value-lo plane per tile in a
+// second array, and per tile the largest error the value hi plane alone
+// leaves (fp32; NaN when a value is not finite).
 constexpr int kPrefillPlanes = 3;
+constexpr int kPrefillLoHalves = 8192;  // halves per value-lo plane
 struct PrefillPlanes {
   _Float16* img;
+  _Float16* img_lo;
+  float* err;  // [B][Hkv][Lp / 64]
   int64_t Lp;  // padded tokens per (sequence, KV head), multiple of 64
 };
+// workspace bytes of one part's PrefillPlanes
+int64_t prefill_planes_bytes(int64_t batch, int64_t n_kv_heads, int64_t Lp);
+// the PrefillPlanes of a part at ws (prefill_planes_bytes long)
+PrefillPlanes prefill_planes_at(char* ws, int64_t batch, int64_t n_kv_heads, int64_t Lp);
 
 // One part as the prefill kernel reads it.
 struct PrefillPart {
   const float* q;               // q_hist or q_exact
   const _Float16* img;
+  const _Float16* img_lo;
+  const float* err;
   const long long* len;         // [batch] tokens per sequence, NULL: max_len
   int64_t max_len, Lp, split_len;
   long long pos_offset;         // absolute position of token 0

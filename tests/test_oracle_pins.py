@@ -198,3 +198,87 @@ def test_blockvq_scores_keys_on_codewords():
     np.testing.assert_allclose(got.double().numpy(), query.double().numpy() @ keys.double().numpy().T,
                                rtol=1e-6, atol=1e-6)
     assert R.blockvq_scores(query.half(), R.BlockQ(idx, 4, 4), dec).dtype == torch.float16
+
+
+# ------------------------------------------ rotation_dequantize / scores ---
+
+def _rotation_encoded(bits, n, seed):
+    """A random orthogonal (non-symmetric) rotation, non-uniform coordinate
+    scales e^[-1.2, 1.2] in shuffled order, midpoint tables, encoded keys
+    (smaq/weighted_scalar.py:347-355)."""
+    g = torch.Generator().manual_seed(seed)
+    rot, _ = torch.linalg.qr(torch.randn(128, 128, generator=g))
+    s = torch.exp(torch.linspace(-1.2, 1.2, 128))[torch.randperm(128, generator=g)]
+    c, _, db = R.midpoint_tables(bits)
+    k = sample_keys(n, seed=seed + 1)
+    return rot, s, c, R.scalar_encode(k, rot, db, bits, coord_scales=s)
+
+
+@pytest.mark.parametrize("bits", [3, 4])
+def test_rotation_dequantize_inverts_the_encoder(bits):
+    """(k_hat / n) R^T * s = c[code]: dequantisation undoes the encoder's
+    rotate-then-scale (smaq/weighted_scalar.py:347-363).  Passing the scales
+    where the inverse scales belong, or R^T for R, fails by a wide margin."""
+    rot, s, c, q = _rotation_encoded(bits, 200, 40)
+    n = q.norms.double().numpy()
+    r64, s64 = rot.double().numpy(), s.double().numpy()
+    want = c.double().numpy()[_bit_loop_codes(q.indices, bits, 128)]
+
+    def back(khat):
+        return (khat.double().numpy() / n[:, None]) @ r64.T * s64[None, :]
+
+    err = np.abs(back(R.rotation_dequantize(q, c, 1.0 / s, rot, 128)) - want).max()
+    assert err < 1e-4
+    assert np.abs(back(R.rotation_dequantize(q, c, s, rot, 128)) - want).max() > 1000 * err
+    assert np.abs(back(R.rotation_dequantize(q, c, 1.0 / s, rot.T.contiguous(), 128)) - want).max() > 1000 * err
+
+
+def test_rotation_scores_closed_form():
+    """dim 8, R a signed permutation (row i holds sign_i at column perm_i, so
+    (q R^T)_i = sign_i q_perm_i), scales powers of two:
+    s[t, j] = scale * n_j * sum_i sign_i q[t, perm_i] / s_i * c[code_ji],
+    codes packed by an explicit loop (smaq/weighted_scalar.py:342-345,
+    365-379).  Scales for inverse scales, R^T for R, a dropped norm or
+    scale all fail."""
+    perm, sign = [3, 0, 6, 1, 7, 2, 5, 4], [1, -1, 1, 1, -1, 1, -1, 1]
+    rot = torch.zeros(8, 8)
+    for i in range(8):
+        rot[i, perm[i]] = sign[i]
+    s = torch.tensor([0.25, 0.5, 1.0, 2.0, 4.0, 0.5, 2.0, 1.0])
+    c, _, _ = R.midpoint_tables(3)
+    g = torch.Generator().manual_seed(44)
+    codes = torch.randint(0, 8, (12, 8), generator=g)
+    packed = torch.zeros(12, 4, dtype=torch.uint8)
+    for j in range(12):
+        for p in range(4):
+            packed[j, p] = int(codes[j, 2 * p]) | (int(codes[j, 2 * p + 1]) << 3)
+    norms = torch.rand(12, generator=g) + 0.5
+    query = torch.randn(2, 8, generator=g)
+    q = R.ScalarQ(packed, norms, 3)
+    got = R.rotation_scores(query, q, c, 1.0 / s, rot, 8, scale=0.7).double().numpy()
+    c64, q64, n64, s64 = c.double().numpy(), query.double().numpy(), norms.double().numpy(), s.double().numpy()
+    want = np.zeros((2, 12))
+    for t in range(2):
+        for j in range(12):
+            want[t, j] = 0.7 * n64[j] * sum(sign[i] * q64[t, perm[i]] / s64[i] * c64[int(codes[j, i])]
+                                            for i in range(8))
+    np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-6 * np.abs(want).max())
+    big = 0.1 * np.abs(want).max()
+    assert np.abs(R.rotation_scores(query, q, c, s, rot, 8, scale=0.7).double().numpy() - want).max() > big
+    assert np.abs(R.rotation_scores(query, q, c, 1.0 / s, rot.T.contiguous(), 8, scale=0.7).double().numpy()
+                  - want).max() > big
+    assert np.abs(R.rotation_scores(query, q, c, 1.0 / s, rot, 8).double().numpy() - want).max() > big
+
+
+def test_rotation_scores_equal_query_dot_reconstructed_key():
+    """The scores equal q . k_hat * scale with k_hat = n u, u solving the
+    encoder's map u R^T * s = c[code] by a float64 linear solve -- neither the
+    oracle's dequantiser nor R's orthogonality is assumed."""
+    rot, s, c, q = _rotation_encoded(4, 100, 41)
+    query = sample_keys(4, seed=43)
+    got = R.rotation_scores(query, q, c, 1.0 / s, rot, 128, scale=0.0884).double().numpy()
+    y = c.double().numpy()[_bit_loop_codes(q.indices, 4, 128)]
+    u = np.linalg.solve(rot.double().numpy(), (y / s.double().numpy()[None, :]).T).T
+    want = query.double().numpy() @ (u * q.norms.double().numpy()[:, None]).T * 0.0884
+    np.testing.assert_allclose(got, want, rtol=0, atol=1e-5 * np.abs(want).max())
+    assert got.shape == (4, 100)

@@ -243,6 +243,28 @@ typedef struct smaq_attn_params {
      decode kernel for single-token queries, the prefill kernel for
      q_len >= 16 at head_dim 128, the generic kernels otherwise. */
   int impl;
+  /* Optional split merge inside the matrix-core decode kernel (NULL: a
+     combine launch merges the splits).  int32 [batch * Hkv] arrival
+     counters, zero before the first call; every call leaves them zero.
+     When the decode kernel serves a history-only call in several splits,
+     each workgroup counts itself in once its partial is written and the
+     last one of its (sequence, KV head) merges the partials in split order
+     (the combine launch's arithmetic) and writes the output: phase 1 then
+     writes the output and phase 4 launches nothing.  Calls sharing the
+     counters must not overlap. */
+  int* arrivals;
+  /* Optional query rotation (rot_mt NULL: q_hist is read as given).  With
+     rot_mt set, phase 1 first writes q_hist = (q_raw @ M^T) [* rot_scale]
+     (smaq_rotate_rows, one launch), the codec-space query that
+     SMAQQuantizer.rotate_query (smaq/quantizer.py:131-136) and
+     RotationAdapter.rotate_query (smaq/weighted_scalar.py:342-345) form
+     before scoring; q_hist must then be a writable fp32 buffer.
+       q_raw [batch][q_len][Hq][D] in q_raw_dtype; rot_mt = M^T [D][D] fp32;
+       rot_scale [D] fp32 or NULL. */
+  const void* q_raw;
+  int q_raw_dtype;
+  const float* rot_mt;
+  const float* rot_scale;
 } smaq_attn_params;
 
 /* Bytes of workspace smaq_attn_hybrid needs for these parameters. */

@@ -52,6 +52,8 @@ class AttnParams(ctypes.Structure):
         ("workspace", c_void_p), ("workspace_bytes", c_ll),
         ("max_hist_len", c_ll), ("max_recent_len", c_ll),
         ("phases", c_int), ("impl", c_int),
+        ("arrivals", c_void_p),
+        ("q_raw", c_void_p), ("q_raw_dtype", c_int), ("rot_mt", c_void_p), ("rot_scale", c_void_p),
     ]
 
 

@@ -491,6 +491,7 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
   if (p.has_history) {
     SMAQ_REQUIRE(p.q_hist && p.key_bytes && p.key_lut && p.val_bytes && p.val_scales && p.val_zeros,
                  "smaq_attn_hybrid: null history pointer");
+    if (p.rot_mt) SMAQ_REQUIRE(p.q_raw, "smaq_attn_hybrid: rot_mt without q_raw");
     SMAQ_REQUIRE(p.val_group > 0 && p.head_dim % p.val_group == 0, "smaq_attn_hybrid: bad value group");
     SMAQ_REQUIRE(p.val_bits >= 1 && p.val_bits <= 8, "smaq_attn_hybrid: bad value bits");
     if (p.block_table) SMAQ_REQUIRE(p.block_size > 0 && p.max_blocks > 0, "smaq_attn_hybrid: bad paging");
@@ -532,8 +533,18 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
 
   const int phases = p.phases ? p.phases : 7;
   // The matrix-core decode kernel writes the output itself when the history
-  // is one split and there is no recent part: no combine launch.
+  // is one split and there is no recent part, or, given arrival counters,
+  // merges its several splits itself (its last workgroup per sequence and KV
+  // head): no combine launch.
   const bool direct = pl.mfma && pl.s_hist == 1 && pl.s_recent == 0;
+  const bool merge = pl.mfma && pl.s_hist > 1 && pl.s_recent == 0 && p.arrivals != nullptr;
+  // The query rotation (given rot_mt) is one launch into q_hist ahead of
+  // the history phase.
+  if (p.has_history && p.rot_mt && (phases & 1)) {
+    const int rc = smaq_rotate_rows(p.q_raw, p.q_raw_dtype, (long long)p.batch * p.q_len * p.n_q_heads, p.head_dim,
+                                    p.rot_mt, p.rot_scale, (float*)p.q_hist, stream);
+    if (rc != SMAQ_OK) return rc;
+  }
   if (pl.prefill) {
     char* ws = (char*)p.workspace + align256(n_part * (p.head_dim + 2) * (int64_t)sizeof(float));
     auto planes = [&](int64_t lp) {
@@ -569,7 +580,7 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
         order = (int*)((char*)p.workspace + align256(partial_bytes(&p, pl)));
         if ((rc = launch_decode_order(p, order, st)) != SMAQ_OK) return rc;
       }
-      rc = launch_mfma_decode(p, a, part, pl.s_hist, direct, order, st);
+      rc = launch_mfma_decode(p, a, part, pl.s_hist, direct, merge, order, st);
       if (rc != SMAQ_OK) return rc;
     } else if (p.key_format == SMAQ_KEY_SCALAR) {
       switch (p.norm_dtype) {
@@ -595,7 +606,7 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
     const int rc = launch_status("smaq_attn_hybrid(recent)");
     if (rc != SMAQ_OK) return rc;
   }
-  if (!(phases & 4) || direct) return SMAQ_OK;
+  if (!(phases & 4) || direct || merge) return SMAQ_OK;
   dim3 cgrid((unsigned)((rows + kCombineRows - 1) / kCombineRows), p.n_kv_heads, p.batch);
   const dim3 cblock((unsigned)((p.head_dim + 63) / 64 * 64), kCombineRows);  // one thread per output dim
   switch (p.out_dtype) {

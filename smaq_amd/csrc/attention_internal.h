@@ -85,8 +85,10 @@ int64_t mfma_decode_split_len(const smaq_attn_params& p);
 // the sequences by history length, longest first.
 int launch_decode_order(const smaq_attn_params& p, int* order, hipStream_t st);
 // With `direct` (one split and no recent part) the kernel writes the final
-// output itself, and no split combine is needed.
+// output itself, and no split combine is needed; with `merge` (several
+// splits, no recent part, p.arrivals set) the last workgroup of each
+// (sequence, KV head) merges the splits and writes the output.
 int launch_mfma_decode(const smaq_attn_params& p, const HistAddr& a, const Partials& part,
-                       int n_splits, bool direct, const int* order, hipStream_t st);
+                       int n_splits, bool direct, bool merge, const int* order, hipStream_t st);
 
 }  // namespace smaq

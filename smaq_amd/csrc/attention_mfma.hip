@@ -55,6 +55,9 @@ constexpr float kLazyRescale = 8.0f;
 // s_waitcnt operand that waits for LDS and scalar loads only (lgkmcnt 0,
 // vmcnt and expcnt at their maxima)
 constexpr int kWaitLdsOnly = 0xC07F;
+// s_waitcnt operand that waits for vector memory operations only (vmcnt 0,
+// expcnt and lgkmcnt at their maxima)
+constexpr int kWaitVmemOnly = 0x0F70;
 
 // Split boundaries.  The grid (KV heads, sequences, splits) is dispatched
 // split-major, so with one round of workgroups, split s of unit u = head +
@@ -71,6 +74,8 @@ struct SplitRule {
   int slots;  // round-slots per CU (at most kMaxSlots)
   int tilt;   // weight step per slot; tilt * (slots - 1) < kSplitWeight
   int direct; // one split and no recent part: write the final output
+  int merge;  // several splits, no recent part, arrival counters given: the
+              // last workgroup of each (sequence, KV head) writes the output
 };
 constexpr int kSplitWeight = 64;
 
@@ -112,6 +117,18 @@ __device__ __forceinline__ int exponent_of(float x) {
   int e;
   frexpf(x, &e);
   return e - 1;
+}
+
+// Workgroup barrier that waits for this wave's LDS operations only (global
+// loads stay in flight).  The compiler barriers on both sides of the wait
+// keep every LDS access of the code around it on its side: the wait
+// intrinsic itself does not order memory operations.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(kWaitLdsOnly);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 // Orders this wave's LDS writes before its later LDS reads of other lanes'
@@ -259,6 +276,43 @@ struct NormPair {
   }
 };
 
+// Two output elements (o0, o1) at element offset oi of the output.
+__device__ __forceinline__ void store_out2(const smaq_attn_params& p, int64_t oi, float o0, float o1) {
+  switch (p.out_dtype) {
+    case SMAQ_F32: {
+      float* o = (float*)p.out + oi;
+      o[0] = o0;
+      o[1] = o1;
+    } break;
+    case SMAQ_F16: {
+      _Float16* o = (_Float16*)p.out + oi;
+      o[0] = Num<_Float16>::from_f(o0);
+      o[1] = Num<_Float16>::from_f(o1);
+    } break;
+    default: {
+      bf16* o = (bf16*)p.out + oi;
+      o[0] = Num<bf16>::from_f(o0);
+      o[1] = Num<bf16>::from_f(o1);
+    } break;
+  }
+}
+
+// Agent-coherent (device-scope relaxed atomic) stores and loads: on gfx950
+// they carry the sc1 cache policy, so a store is written through the XCD's
+// L2 and a load misses a stale L2 line, without cache-wide maintenance.
+__device__ __forceinline__ void store_agent(float* a, float v) {
+  __hip_atomic_store((uint32_t*)a, __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_agent(float* a, f32x2 v) {
+  __hip_atomic_store((uint64_t*)a, __builtin_bit_cast(uint64_t, v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float* a) {
+  return __builtin_bit_cast(float, __hip_atomic_load((const uint32_t*)a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ f32x2 load_agent2(const float* a) {
+  return __builtin_bit_cast(f32x2, __hip_atomic_load((const uint64_t*)a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
 template <int KBITS, typename TN, typename TV, bool SPLIT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWaves<TN, TV>, kDecodeWaves<TN, TV>))) void decode_mfma_kernel(
     smaq_attn_params p, HistAddr addr, Partials part, SplitRule rule, const int* __restrict__ order) {
@@ -273,6 +327,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
   __shared__ __attribute__((aligned(16))) uint8_t ast[kMWaves][16 * kARow];
   __shared__ float red_m[kMWaves][4];
   __shared__ float red_l[kMWaves][4];
+  __shared__ int last_split;  // merge: this workgroup is its unit's last arrival
   // per-wave results, laid over the spread tiles once every wave has left its loop
   float (*const red_o)[4][128] = (float (*)[4][128])&vsp[0][0];
 
@@ -321,7 +376,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
   // issued together: the query rows first, as vector loads; the centroids as
   // scalar loads, each lane taking its table entries from them by index.
   const int qrow = n < Q ? n : ((n >= 8 && n < 8 + Q) ? n - 8 : -1);
-  const float* qsrc = p.q_hist + ((int64_t)b * p.n_q_heads + h * Q + (qrow < 0 ? 0 : qrow)) * 128;
+  const int64_t qrow0 = (int64_t)b * p.n_q_heads + h * Q;  // first query row of this KV head
+  const float* qsrc = p.q_hist + (qrow0 + (qrow < 0 ? 0 : qrow)) * 128;
   // (padding columns read query row 0 and drop it: loads without a branch)
   float qv[32];
 #pragma unroll
@@ -578,10 +634,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
   // from column qq (its hi column)
   const float rfac = __shfl(p.scale * kLog2e * ldexpf(1.0f, e_q + e_lut), qq, 64);
   // LDS-only barrier: the first tile's global loads stay in flight
-  __builtin_amdgcn_s_waitcnt(kWaitLdsOnly);
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
+  lds_barrier();
 
   // reference max / running sum of query row qq (max replicated over its 16
   // lanes; the sum is this lane's share, reduced once at the end)
@@ -904,33 +957,91 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
       // the output itself: the split combine's arithmetic for one partial
       // (o * (1 / l), zero without tokens), in the output dtype
       const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-      const float r0 = O[0] * inv, r1 = O[1] * inv;
-      const int64_t oi = ((int64_t)b * p.n_q_heads + h * Q + j) * 128 + d;
-      switch (p.out_dtype) {
-        case SMAQ_F32: {
-          float* o = (float*)p.out + oi;
-          o[0] = r0;
-          o[1] = r1;
-        } break;
-        case SMAQ_F16: {
-          _Float16* o = (_Float16*)p.out + oi;
-          o[0] = Num<_Float16>::from_f(r0);
-          o[1] = Num<_Float16>::from_f(r1);
-        } break;
-        default: {
-          bf16* o = (bf16*)p.out + oi;
-          o[0] = Num<bf16>::from_f(r0);
-          o[1] = Num<bf16>::from_f(r1);
-        } break;
-      }
+      store_out2(p, (qrow0 + j) * 128 + d, O[0] * inv, O[1] * inv);
     } else {
       const int64_t pi = part.idx(b, h, p.n_kv_heads, Q, j, s);
-      *(f32x2*)&part.o[pi * 128 + d] = O;
-      if (d == 0) {
-        part.m[pi] = M == -__builtin_inff() ? M : M * 0.6931471805599453f;
-        part.l[pi] = L;
+      const float Mn = M == -__builtin_inff() ? M : M * 0.6931471805599453f;
+      if (rule.merge) {
+        // agent-coherent stores (written through this XCD's L2), read back by
+        // the merging workgroup with agent-coherent loads
+        store_agent(&part.o[pi * 128 + d], O);
+        if (d == 0) {
+          store_agent(&part.m[pi], Mn);
+          store_agent(&part.l[pi], L);
+        }
+      } else {
+        *(f32x2*)&part.o[pi * 128 + d] = O;
+        if (d == 0) {
+          part.m[pi] = Mn;
+          part.l[pi] = L;
+        }
       }
     }
+  }
+  if (!rule.merge) return;
+  // ---- split merge.  Once every thread has seen its agent-coherent partial
+  // stores complete (vmcnt 0), one thread counts the workgroup in with a
+  // vector atomic; the workgroup that completes the count is the unit's
+  // last, resets the counter for the next call and merges all splits in
+  // split order with the combine kernel's arithmetic, so the result does not
+  // depend on which workgroup arrives last.  No cache-wide fence: a device-
+  // scope release / acquire writes back / invalidates the whole L2 of the
+  // XCD in every workgroup (measured: 178 -> 313 us at c3).
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(kWaitVmemOnly);
+  asm volatile("" ::: "memory");
+  __syncthreads();
+  if (tid == 0) {
+    int* const cnt = p.arrivals + ((int64_t)b * p.n_kv_heads + h);
+    const int before = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = before == rule.n_splits - 1 ? 1 : 0;
+    if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_split = last;
+  }
+  __syncthreads();
+  if (!last_split) return;
+  const int S = part.S;
+  for (int i = tid; i < Q * 64; i += 256) {
+    const int j = i >> 6, d = 2 * (i & 63);
+    const int64_t base = part.idx(b, h, p.n_kv_heads, Q, j, 0);
+    float M = -__builtin_inff(), L = 0.0f, o0 = 0.0f, o1 = 0.0f;
+    for (int c0 = 0; c0 < S; c0 += 8) {
+      // a chunk's loads are all issued before any is used
+      float mv[8], lv[8];
+      f32x2 ov[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        lv[k] = 0.0f;
+        mv[k] = -__builtin_inff();
+        ov[k] = f32x2{0.0f, 0.0f};
+        if (c0 + k < S) {
+          lv[k] = load_agent(&part.l[base + c0 + k]);
+          mv[k] = load_agent(&part.m[base + c0 + k]);
+          ov[k] = load_agent2(&part.o[(base + c0 + k) * 128 + d]);
+        }
+      }
+      float Mc = M;
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (lv[k] > 0.0f) Mc = fmaxf(Mc, mv[k]);
+      if (Mc > M) {
+        const float c = __expf(M - Mc);
+        L *= c;
+        o0 *= c;
+        o1 *= c;
+        M = Mc;
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        if (!(lv[k] > 0.0f)) continue;
+        const float wk = __expf(mv[k] - M);
+        L = fmaf(lv[k], wk, L);
+        o0 += ov[k][0] * wk;
+        o1 += ov[k][1] * wk;
+      }
+    }
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    store_out2(p, (qrow0 + j) * 128 + d, o0 * inv, o1 * inv);
   }
 }
 
@@ -1044,7 +1155,7 @@ static void launch_n(const smaq_attn_params& p, const HistAddr& a, const Partial
 }
 
 int launch_mfma_decode(const smaq_attn_params& p, const HistAddr& a, const Partials& part,
-                       int n_splits, bool direct, const int* order, hipStream_t st) {
+                       int n_splits, bool direct, bool merge, const int* order, hipStream_t st) {
   const bool wide = p.norm_dtype == SMAQ_F32 || p.val_dtype == SMAQ_F32;
   SplitRule rule;
   rule.n_splits = n_splits;
@@ -1052,6 +1163,7 @@ int launch_mfma_decode(const smaq_attn_params& p, const HistAddr& a, const Parti
   rule.slots = wide ? 3 : 4;
   rule.tilt = wide ? 0 : kSplitTilt4;
   rule.direct = direct && n_splits == 1 ? 1 : 0;
+  rule.merge = merge && !rule.direct && p.arrivals ? 1 : 0;
   if (p.key_bits == 3) launch_n<3>(p, a, part, rule, n_splits, order, st);
   else launch_n<4>(p, a, part, rule, n_splits, order, st);
   return launch_status("smaq_attn_hybrid(mfma decode)");

@@ -160,41 +160,43 @@ __global__ __launch_bounds__(256) void rotate_rows128_kernel(const T* __restrict
   out[r * 128 + j] = s ? acc * s[j] : acc;
 }
 
-// Many rows at head_dim 128 (a decode step of thousands of sequences): the
-// 2-row blocks above read the 64 KB matrix once per row from L2, so here a
-// block of 128 threads (one per column j) holds 8 rows and each Mt element
-// feeds 8 chains.  Each chain is the same sequential fmaf over d, so both
-// kernels give the same bits.
-constexpr int kRot128Rows = 8;
-constexpr int64_t kRot128ManyRows = 4096;  // from this many rows on
+// More rows at head_dim 128 (a decode step of a thousand or more query
+// rows): the 2-row blocks above read the 64 KB matrix once per row pair from
+// L2, so here a block of 128 threads (one per column j) holds ROWS rows and
+// each Mt element feeds ROWS chains; the Mt loads go out CHUNK at a time.
+// Each chain is the same sequential fmaf over d, so every kernel gives the
+// same bits.  8 rows from kRot128ManyRows rows on; 4 rows (one block per CU
+// at 1024 rows, half the L2 reads of the 2-row blocks) from kRot128MidRows.
+constexpr int64_t kRot128ManyRows = 4096;
+constexpr int64_t kRot128MidRows = 512;
 
-template <typename T>
-__global__ __launch_bounds__(128) void rotate_rows128x8_kernel(const T* __restrict__ x, int64_t rows,
-                                                               const float* __restrict__ Mt,
-                                                               const float* __restrict__ s,
-                                                               float* __restrict__ out) {
-  __shared__ float xs[kRot128Rows][128];
+template <typename T, int ROWS, int CHUNK>
+__global__ __launch_bounds__(128) void rotate_rows128_multi_kernel(const T* __restrict__ x, int64_t rows,
+                                                                   const float* __restrict__ Mt,
+                                                                   const float* __restrict__ s,
+                                                                   float* __restrict__ out) {
+  __shared__ float xs[ROWS][128];
   const int j = threadIdx.x;
-  const int64_t r0 = (int64_t)blockIdx.x * kRot128Rows;
+  const int64_t r0 = (int64_t)blockIdx.x * ROWS;
 #pragma unroll
-  for (int i = 0; i < kRot128Rows; ++i) xs[i][j] = r0 + i < rows ? Num<T>::to_f(x[(r0 + i) * 128 + j]) : 0.0f;
+  for (int i = 0; i < ROWS; ++i) xs[i][j] = r0 + i < rows ? Num<T>::to_f(x[(r0 + i) * 128 + j]) : 0.0f;
   __syncthreads();
-  float acc[kRot128Rows];
+  float acc[ROWS];
 #pragma unroll
-  for (int i = 0; i < kRot128Rows; ++i) acc[i] = 0.0f;
+  for (int i = 0; i < ROWS; ++i) acc[i] = 0.0f;
 #pragma unroll
-  for (int d0 = 0; d0 < 128; d0 += 32) {
-    float m[32];
+  for (int d0 = 0; d0 < 128; d0 += CHUNK) {
+    float m[CHUNK];
 #pragma unroll
-    for (int i = 0; i < 32; ++i) m[i] = Mt[(d0 + i) * 128 + j];
+    for (int i = 0; i < CHUNK; ++i) m[i] = Mt[(d0 + i) * 128 + j];
 #pragma unroll
-    for (int i = 0; i < 32; ++i)
+    for (int i = 0; i < CHUNK; ++i)
 #pragma unroll
-      for (int r = 0; r < kRot128Rows; ++r) acc[r] = fmaf(xs[r][d0 + i], m[i], acc[r]);
+      for (int r = 0; r < ROWS; ++r) acc[r] = fmaf(xs[r][d0 + i], m[i], acc[r]);
   }
   const float sj = s ? s[j] : 1.0f;
 #pragma unroll
-  for (int r = 0; r < kRot128Rows; ++r)
+  for (int r = 0; r < ROWS; ++r)
     if (r0 + r < rows) out[(r0 + r) * 128 + j] = s ? acc[r] * sj : acc[r];
 }
 
@@ -360,7 +362,15 @@ extern "C" int smaq_rotate_rows(const void* x, int xdtype, long long rows, int D
   hipStream_t st = (hipStream_t)stream;
   if (D == 128 && rows >= kRot128ManyRows) {
     SMAQ_DISPATCH_DTYPE(xdtype, T,
-        hipLaunchKernelGGL(rotate_rows128x8_kernel<T>, dim3((unsigned)((rows + kRot128Rows - 1) / kRot128Rows)),
+        hipLaunchKernelGGL((rotate_rows128_multi_kernel<T, 8, 32>), dim3((unsigned)((rows + 7) / 8)),
+                           dim3(128), 0, st, (const T*)x, (int64_t)rows, Mt, coord_scales, out);
+        return launch_status("smaq_rotate_rows");)
+    set_error("smaq_rotate_rows: unsupported dtype %d", xdtype);
+    return SMAQ_EUNSUPPORTED;
+  }
+  if (D == 128 && rows >= kRot128MidRows) {
+    SMAQ_DISPATCH_DTYPE(xdtype, T,
+        hipLaunchKernelGGL((rotate_rows128_multi_kernel<T, 4, 64>), dim3((unsigned)((rows + 3) / 4)),
                            dim3(128), 0, st, (const T*)x, (int64_t)rows, Mt, coord_scales, out);
         return launch_status("smaq_rotate_rows");)
     set_error("smaq_rotate_rows: unsupported dtype %d", xdtype);

@@ -106,14 +106,25 @@ class AttentionPlan:
         p.hist_pos_offset = int(hist_pos_offset)
         p.recent_pos_offset = int(recent_pos_offset)
         self.q_hist = None
+        self.rot_t = None
+        self._q_raw = None
         if has_hist:
             if fused.rot_t is not None:
+                # The library rotates the raw query itself (inside the decode
+                # kernel when that kernel serves the call, else by one launch
+                # into q_hist).
                 self.q_hist = torch.empty_like(self.q_exact)
                 self.rot_t = fused.rot_t.to(dev, torch.float32).contiguous()
                 self.rot_scale = None if fused.rot_scale is None else fused.rot_scale.to(dev, torch.float32).contiguous()
                 p.q_hist = self.q_hist.data_ptr()
+                p.rot_mt = self.rot_t.data_ptr()
+                p.rot_scale = None if self.rot_scale is None else self.rot_scale.data_ptr()
             else:
                 p.q_hist = self.q_exact.data_ptr()
+            # split arrival counters (zero; every call leaves them zero): the
+            # decode kernel merges its own splits, no combine launch
+            self.arrivals = torch.zeros(B * n_kv_heads, dtype=torch.int32, device=dev)
+            p.arrivals = self.arrivals.data_ptr()
             p.has_history = 1
             p.key_bytes = key_codes.data_ptr()
             p.key_row_bytes = key_codes.shape[-1]
@@ -174,15 +185,21 @@ class AttentionPlan:
         self._keep = keep
 
     def load_query(self, query: torch.Tensor) -> None:
-        """Copy a query in and prepare the codec-space query.  With a rotated
-        codec the rotate kernel reads the query in its own dtype; the fp32 copy
-        is made only when the exact (recent-window) path or an unrotated
-        codec reads it."""
+        """Hand a query to the plan.  With a rotated codec the library reads
+        the query as given (fp32/fp16/bf16, contiguous, 16-byte aligned;
+        anything else is copied to fp32 first) and rotates it during the
+        launch; the fp32 copy is made only when the exact (recent-window) path
+        or an unrotated codec reads it."""
         q = query.reshape(self.shape)
-        if self.q_hist is not None:
-            if q.dtype not in (torch.float32, torch.float16, torch.bfloat16) or not q.is_contiguous():
-                q = q.to(torch.float32).contiguous()
-            _native.rotate_rows_into(q, self.rot_t, self.rot_scale, self.q_hist)
+        if self.rot_t is not None:
+            if q.device != self.device:
+                q = q.to(self.device)
+            if (q.dtype not in (torch.float32, torch.float16, torch.bfloat16) or not q.is_contiguous()
+                    or q.data_ptr() % 16):
+                q = q.to(torch.float32).clone(memory_format=torch.contiguous_format)
+            self._q_raw = q  # kept alive until the next load
+            self.params.q_raw = q.data_ptr()
+            self.params.q_raw_dtype = _native.dtype_code(q.dtype)
             if self.needs_exact:
                 self.q_exact.copy_(q)
         else:

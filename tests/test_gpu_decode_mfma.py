@@ -209,3 +209,47 @@ def test_mfma_unsupported_shape_raises(dev):
     q = torch.randn(1, 2, 16, 128)         # 2 query tokens: not a decode shape
     with pytest.raises(RuntimeError, match="matrix-core"):
         kvb.attention(q.to(dev), impl=2)
+
+
+@pytest.mark.parametrize("qdtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_mfma_decode_split_merge(dev, qdtype):
+    """Several splits per (sequence, KV head) and a rotated codec: the plan
+    hands the raw query to the library (which rotates it into q_hist) and
+    gives arrival counters, so the decode kernel's last workgroup per unit
+    merges the splits.  The output is bit-identical to the separate launches
+    (rotation by the caller, decode partials, combine kernel), the counters
+    are zero again after every call (a second run gives the same bits), and
+    sampled sequences match the oracle."""
+    from smaq_amd import _native
+    strat, codec = _codec_pair(dev, 3, 340)
+    hkv, g = 8, 4
+    lens = [6000, 4097, 5555]
+    gen = torch.Generator().manual_seed(341)
+    keys = [sample_keys(n * hkv, seed=342 + i).reshape(n, hkv, 128).bfloat16() for i, n in enumerate(lens)]
+    vals = [torch.randn(n, hkv, 128, generator=gen).bfloat16() for n in lens]
+    kvb = QuantizedKVBatch.encode(strat, [k.to(dev) for k in keys], [v.to(dev) for v in vals])
+    q = torch.randn(len(lens), hkv * g, 128, generator=gen).to(qdtype)
+    qd = q.to(dev)
+    plan = kvb.plan(qd, impl=2)
+    assert plan.rot_t is not None and plan.params.rot_mt, "codec without rotation"
+    # the plan's workspace holds more than one split per unit: the merge path
+    one_split = len(lens) * hkv * g * (128 + 2) * 4
+    assert plan.workspace.numel() > one_split
+    out1 = plan.run(qd).clone()
+    out2 = plan.run(qd).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(out1, out2), "second call differs (arrival counters not reset?)"
+    assert int(plan.arrivals.abs().sum()) == 0
+    # separate launches: rotation by the caller, partials, combine
+    plan.params.arrivals = None
+    plan.params.rot_mt = None
+    plan.params.rot_scale = None
+    plan.q_hist.zero_()
+    _native.rotate_rows_into(qd.reshape(plan.shape).contiguous(), plan.rot_t, plan.rot_scale, plan.q_hist)
+    plan.out.zero_()
+    ref = plan.launch().clone()
+    torch.cuda.synchronize()
+    assert torch.equal(out1, ref), f"split merge differs: {(out1.float() - ref.float()).abs().max()}"
+    for b in (0, 2):
+        assert_attn_close(out1[b:b + 1], _oracle(codec, keys[b], vals[b], q[b:b + 1], hkv * g, hkv),
+                          f"split merge {qdtype} seq {b}")

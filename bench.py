@@ -222,6 +222,7 @@ def bench_decode(args, dev):
     achieved = algo_bytes / (kern * 1e-3) / 1e9
     cpu = None if args.no_cpu_baseline else cpu_baseline_decode(strat, keys, vals, q, Hq, Hkv, D, bits)
     del keys, vals
+    ring = bench_decode_ring(args, kvb, q, Hkv, D, algo_bytes)
     return _record(
         args, value=B / (ms_step * 1e-3), unit="tokens/s", ms_step=ms_step, dtype=DECODE_DTYPE,
         data="synthetic (seeded N(0, U diag(1/i) U^T) keys, N(0,1) values)",
@@ -235,7 +236,30 @@ def bench_decode(args, dev):
                   "algorithmic_bytes": algo_bytes, "bytes_per_token_head": bytes_per_th},
         cpu=cpu, settle_info=st,
         extra={"encode_cache_s": encode_s, "encode_boundary_ties": ties,
-               "hbm_gbs_whole_step": algo_bytes / (ms_step * 1e-3) / 1e9})
+               "hbm_gbs_whole_step": algo_bytes / (ms_step * 1e-3) / 1e9, "c3_ring128": ring})
+
+
+def bench_decode_ring(args, kvb, q, Hkv, D, hist_bytes, R: int = 128):
+    """c3 with the exact recent ring the vLLM adapter always serves beside
+    the history (1..128 tokens; here full, 128 bf16 tokens per sequence): the
+    history phase writes split partials, the recent phase adds one partial
+    per (sequence, KV head), the combine merges them.  Same step definition
+    as the headline; phases timed apart on the launch stream."""
+    dev = q.device
+    B = q.shape[0]
+    g = torch.Generator(device=dev).manual_seed(14)
+    rk = torch.randn(B, R, Hkv, D, generator=g, device=dev).bfloat16()
+    rv = torch.randn(B, R, Hkv, D, generator=g, device=dev).bfloat16()
+    plan = kvb.plan(q, recent_k=rk, recent_v=rv)
+    ms_step, st = time_steps(lambda: plan.run(q), args)
+    plan.load_query(q)
+    phase = {name: kernel_ms(lambda m=m: plan.launch(phases=m), args.steps)
+             for name, m in (("history_ms", 1), ("recent_ms", 2), ("combine_ms", 4))}
+    byts = hist_bytes + B * R * Hkv * D * 2 * 2
+    return {"value": B / (ms_step * 1e-3), "unit": "tokens/s", "ms_per_step": ms_step,
+            "config": {"workload": "c3 + exact recent ring", "recent_tokens": R, "recent_dtype": "bf16"},
+            "hbm_gbs_whole_step": byts / (ms_step * 1e-3) / 1e9, "algorithmic_bytes": byts,
+            "phases": phase, "settle": st}
 
 
 def cpu_baseline_decode(strat, keys, vals, q, Hq, Hkv, D, bits):
@@ -289,6 +313,7 @@ def bench_paged(args, dev):
     achieved = algo / (kern * 1e-3) / 1e9
     cpu = None if args.no_cpu_baseline else cpu_baseline_paged(strat, table, lens, bs, codes, norms, vd, vsc, vz,
                                                                   q, Hq, Hkv, D)
+    adapter = bench_paged_adapter(args, strat, codes, norms, vd, vsc, vz, table, lens, total, q, plan, ms_step)
     return _record(
         args, value=B / (ms_step * 1e-3), unit="tokens/s", ms_step=ms_step, dtype=DECODE_DTYPE,
         data="synthetic (Student-t(3) keys, N(0,1) values, seeded lengths and block tables)",
@@ -300,7 +325,66 @@ def bench_paged(args, dev):
                   "traffic": recorded_traffic("decode_mfma_paged_c5", dict(seqs=B, total_tokens=int(lens.sum()))),
                   "kernel": "decode_mfma_kernel (paged)", "kernel_ms": kern, "algorithmic_bytes": algo,
                   "bytes_per_token_head": pk.nbytes_per_token_head()},
-        cpu=cpu, settle_info=st, extra={"encode_boundary_ties": strat.quantizer.tie_counter.value()})
+        cpu=cpu, settle_info=st, extra={"encode_boundary_ties": strat.quantizer.tie_counter.value(),
+                                         "adapter": adapter})
+
+
+class _FlashImpl:
+    """The attributes of a vLLM flash attention impl that the adapter's hooks
+    read (vLLM is not installed); its own forward never runs in hybrid mode."""
+
+    def __init__(self, num_heads, num_kv_heads, head_size):
+        self.num_heads, self.num_kv_heads, self.head_size = num_heads, num_kv_heads, head_size
+        self.scale = head_size ** -0.5
+
+    def do_kv_cache_update(self, layer, key, value, kv_cache, slot_mapping):
+        pass
+
+    def forward(self, layer, query, key, value, kv_cache, attn_metadata, output=None, output_scale=None,
+                output_block_scale=None):
+        raise RuntimeError("the layer's own attention ran: the SMAQ paged decode did not serve the step")
+
+
+def bench_paged_adapter(args, strat, codes, norms, vd, vsc, vz, table, lens, total, q, plan, ms_plan):
+    """c5 through the vLLM adapter: hooks installed (paged, hybrid) on a
+    one-layer runner whose layer pools are the workload's encoded pools, and
+    each step is the hooked attention forward with vLLM's decode metadata
+    (int32 seq_lens and block table, a [B, Hq * D] query, an output buffer):
+    the adapter's cached plan, its length and table rebinding and the direct
+    write into the output, against plan.run on the same pools."""
+    from types import SimpleNamespace
+    import smaq_amd.integration.vllm as V
+    dev = q.device
+    B, Hq, D = q.shape
+    Hkv, bs = codes.shape[1], codes.shape[2]
+    impl = _FlashImpl(Hq, Hkv, D)
+    ctx = {"layer0": SimpleNamespace(impl=impl, num_heads=Hq)}
+    runner = SimpleNamespace(compilation_config=SimpleNamespace(static_forward_context=ctx), device=dev,
+                             kv_caches=[])
+    state = V.install_hooks(runner, key_bits=3, initial_layers_count=0, mode=V.MODE_HYBRID, paged=True)["layer0"]
+    state.store.key_strategy = strat
+    state.store.quantizer = strat
+    pc = state.paged
+    pc.pools = {"k_codes": codes.view(-1, codes.shape[-1]), "k_norms": norms.view(-1),
+                "v_data": vd.view(-1, vd.shape[-1]), "v_scales": vsc.view(-1, vsc.shape[-1]),
+                "v_zeros": vz.view(-1, vz.shape[-1])}
+    pc.num_blocks, pc.block_size = total, bs
+    meta = SimpleNamespace(num_actual_tokens=B, max_query_len=1, seq_lens=lens.to(dev, torch.int32),
+                           block_table=table.to(dev, torch.int32), max_seq_len=int(lens.max()))
+    qf = q.reshape(B, Hq * D)
+    out = torch.empty(B, Hq * D, dtype=q.dtype, device=dev)
+
+    def step():
+        impl.forward(None, qf, None, None, None, meta, output=out)
+
+    ms_step, st = time_steps(step, args)
+    want = plan.run(q).reshape(B, Hq * D)
+    torch.cuda.synchronize()
+    diff = (out.float() - want.float()).abs().max().item()
+    return {"value": B / (ms_step * 1e-3), "unit": "tokens/s", "ms_per_step": ms_step,
+            "vs_plan_run": ms_plan / ms_step, "max_abs_diff_vs_plan_run": diff,
+            "plans_built": len(pc._plans), "settle": st,
+            "path": "install_hooks(paged=True) + hooked impl.forward (PagedLayerCache.decode)"}
 
 
 class _FlatStore:
@@ -460,8 +544,9 @@ def bench_encode(args, dev):
     v_ms = kernel_ms(lambda: quantize_values(vals, bits=2, group_size=32), args.steps)
     bytes_per_th = 2 * D * 2 + 16 + 32 + 16      # K + V in; indices, codes, scales/zeros out
     algo = rows * bytes_per_th
+    # per token-block: the 8 x 8 metric rotation and the 256-centroid x 8-dim
+    # distance contraction, 2 flops per multiply-add
     flops = rows * 16 * (8 * 8 + 256 * 8) * 2
-    dist_flops = rows * 16 * 256 * 8 * 2
     ties = strat.quantizer.tie_counter.value()
     cpu = None if args.no_cpu_baseline else cpu_baseline_encode(strat, keys, vals)
     del keys, vals
@@ -473,13 +558,13 @@ def bench_encode(args, dev):
                 "kv_heads": H, "head_dim": D, "block_dim": 8, "n_centroids": 256, "storage_dtype": "bf16",
                 "codebook_fit": f"k-means++ on {args.fit_samples} samples, {args.fit_iters} Lloyd iterations "
                                 f"({fit_how}, {t_fit:.1f} s, untimed)"},
-        # the fp32-accurate distance contraction (8 dims x 256 centroids x 2
-        # per token-block) against the FP32 matrix peak; the kernel issues it
-        # as f16 hi/lo products (one 16x16x32 f16 MFMA per 16 centroids x 16
+        # the fp32-accurate rotation + distance contraction (algorithmic_flops)
+        # against the FP32 matrix peak; the kernel issues the distances as
+        # f16 hi/lo products (one 16x16x32 f16 MFMA per 16 centroids x 16
         # tokens), and its limiter is VALU issue for the argmin
         roofline={"bound": "mfma", "kernel": "encode_blockvq_mfma_kernel", "kernel_ms": k_ms,
-                  "achieved": dist_flops / (k_ms * 1e-3) / 1e12, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
-                  "frac": dist_flops / (k_ms * 1e-3) / 1e12 / FP32_PEAK_TFLOPS,
+                  "achieved": flops / (k_ms * 1e-3) / 1e12, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                  "frac": flops / (k_ms * 1e-3) / 1e12 / FP32_PEAK_TFLOPS,
                   "traffic": recorded_traffic("encode_blockvq_c2", dict(rows=rows)), "pack_values_ms": v_ms,
                   "hbm_gbs": algo / ((k_ms + v_ms) * 1e-3) / 1e9, "algorithmic_bytes": algo,
                   "algorithmic_flops": flops,
@@ -503,19 +588,21 @@ def cpu_baseline_encode(strat, keys, vals, n: int = 2048):
 
 # ---------------------------------------------------------- HBM ceiling ---
 
-def copy_ceiling(dev, nbytes: int = 1 << 30, reps: int = 10):
-    """Device-to-device copy of nbytes (read + write bytes / time) and a
-    full fp32 reduction over the same bytes (read only): the practical HBM
-    ceilings next to the 8 TB/s peak, and the reference kernel for counter
-    calibration."""
+def copy_ceiling(dev, nbytes: int = 1 << 30, reps: int = 20):
+    """The practical HBM ceilings next to the 8 TB/s peak: a plain streaming
+    read of nbytes (smaq_probe_read, 16-byte loads over the whole device; the
+    read-bound kernels' ceiling) and a device-to-device copy (read + write
+    bytes / time; also the counter-calibration kernel), each the mean of
+    `reps` back-to-back launches between HIP events on the launch stream."""
+    from smaq_amd import _native
     src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
     dst = torch.empty_like(src)
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
     ms = kernel_ms(lambda: dst.copy_(src), reps)
-    xf = src.view(torch.float32)
-    rms = kernel_ms(lambda: xf.sum(), reps)
+    rms = kernel_ms(lambda: _native.probe_read(src, sink), reps)
     del src, dst
     return {"copy_bytes": nbytes, "copy_ms": ms, "copy_gbs": 2 * nbytes / (ms * 1e-3) / 1e9,
-            "read_ms": rms, "read_gbs": nbytes / (rms * 1e-3) / 1e9}
+            "read_ms": rms, "read_gbs": nbytes / (rms * 1e-3) / 1e9, "read_kernel": "smaq_probe_read"}
 
 
 def _summary(rec: dict) -> dict:

@@ -234,7 +234,10 @@ typedef struct smaq_attn_params {
      Phases communicate through the workspace, launched in order on one
      stream.  When the matrix-core decode kernel serves the history as one
      split per (sequence, KV head) and there is no recent part, phase 1
-     writes the output itself and phase 4 launches nothing. */
+     writes the output itself and phase 4 launches nothing; with arrival
+     counters (below) it merges several splits itself, and, when one call
+     launches phases 1 and 2, the recent partials too (the recent phase then
+     runs first). */
   int phases;
   /* kernel choice: 0 = automatic (matrix-core decode kernel when the shape
      allows, generic kernels otherwise), 1 = generic kernels only, 2 = the
@@ -246,7 +249,8 @@ typedef struct smaq_attn_params {
   /* Optional split merge inside the matrix-core decode kernel (NULL: a
      combine launch merges the splits).  int32 [batch * Hkv] arrival
      counters, zero before the first call; every call leaves them zero.
-     When the decode kernel serves a history-only call in several splits,
+     When the decode kernel serves the history in several splits, or with a
+     recent part whose partials the same call's recent phase wrote first,
      each workgroup counts itself in once its partial is written and the
      last one of its (sequence, KV head) merges the partials in split order
      (the combine launch's arithmetic) and writes the output: phase 1 then
@@ -287,6 +291,16 @@ int smaq_attn_hybrid(const smaq_attn_params* p, void* stream);
  */
 #define SMAQ_NOALLOC_SCRATCH_BYTES (32ll << 20)
 int smaq_attn_hybrid_noalloc(const smaq_attn_params* p, void* stream);
+
+/*
+ * Streaming-read probe.  No counterpart in the reference: a measurement
+ * utility that reads `bytes` (a multiple of 16) from `src` once in 16-byte
+ * loads over the whole device and writes nothing unless the XOR of
+ * everything read equals a fixed sentinel (then one word of `sink`); its
+ * duration gives the HBM read rate a plain stream reaches on this GPU, the
+ * practical ceiling next to the published peak.
+ */
+int smaq_probe_read(const void* src, long long bytes, unsigned int* sink, void* stream);
 
 #ifdef __cplusplus
 }

@@ -83,6 +83,7 @@ _SIGS = {
     "smaq_attn_workspace_bytes": (c_ll, [ctypes.POINTER(AttnParams)]),
     "smaq_attn_hybrid": (c_int, [ctypes.POINTER(AttnParams), c_void_p]),
     "smaq_attn_hybrid_noalloc": (c_int, [ctypes.POINTER(AttnParams), c_void_p]),
+    "smaq_probe_read": (c_int, [c_void_p, c_ll, c_void_p, c_void_p]),
 }
 
 # Size of the built-in workspace of smaq_attn_hybrid_noalloc
@@ -464,6 +465,16 @@ def attn_workspace_bytes(p: AttnParams) -> int:
 def attn_hybrid(p: AttnParams, device: torch.device) -> None:
     """Launches the fused attention described by p (workspace already set)."""
     _check(lib().smaq_attn_hybrid(ctypes.byref(p), _stream(device)), "smaq_attn_hybrid")
+
+
+def probe_read(x: torch.Tensor, sink: torch.Tensor) -> None:
+    """Streaming read of x's bytes (smaq_probe_read), launched on the current
+    stream; sink is a 4-byte-or-larger device tensor the probe may write."""
+    require_gpu(x, sink)
+    if not x.is_contiguous():
+        raise ValueError("probe_read needs a contiguous tensor")
+    nbytes = x.numel() * x.element_size() // 16 * 16
+    _check(lib().smaq_probe_read(_ptr(x), nbytes, _ptr(sink), _stream(x.device)), "smaq_probe_read")
 
 
 def attn_hybrid_noalloc(p: AttnParams, device: torch.device) -> None:

@@ -214,8 +214,17 @@ __global__ __launch_bounds__(kAttnThreads) void attn_recent_kernel(smaq_attn_par
   __shared__ float sc[kRowTile][kChunk];
   __shared__ float m_s[kRowTile], l_s[kRowTile], alpha_s[kRowTile];
   __shared__ long long qpos[kRowTile];
+  // keys of one chunk, transposed ([dim][token], row pitch kChunk + 1 so
+  // that both the staging writes and the score reads are free of bank
+  // conflicts), for head_dim <= kStagedDim: the score loop then reads LDS
+  // instead of one 2- or 4-byte global load per dim from a different row
+  // in every lane
+  constexpr int kStagedDim = 128;
+  constexpr int kKT = kChunk + 1;
+  __shared__ float kT[kStagedDim * kKT];
 
   const int D = p.head_dim;
+  const bool staged = D <= kStagedDim;
   const int g = p.n_q_heads / p.n_kv_heads;
   const int rows = p.q_len * g;
   const int s = blockIdx.x;
@@ -254,10 +263,29 @@ __global__ __launch_bounds__(kAttnThreads) void attn_recent_kernel(smaq_attn_par
   for (int64_t c0 = t0; c0 < t1; c0 += kChunk) {
     const int64_t t = c0 + st;
     const bool valid = t < t1;
+    if (staged) {
+      // coalesced row reads (consecutive dims in consecutive lanes); the
+      // previous chunk's readers passed the barrier at the loop end
+      const int nt = (int)min((int64_t)kChunk, t1 - c0);
+      const int per = kAttnThreads / D, d = tid % D;  // D divides kAttnThreads
+      const TR* kc = rk + c0 * tstride + (int64_t)h * D + d;
+#pragma unroll 8
+      for (int tk = tid / D; tk < nt; tk += per) kT[d * kKT + tk] = Num<TR>::to_f(kc[tk * tstride]);
+      __syncthreads();
+    }
     float acc[kRowTile / 4];
 #pragma unroll
     for (int i = 0; i < kRowTile / 4; ++i) acc[i] = 0.0f;
-    if (valid) {
+    if (valid && staged) {
+      for (int d = 0; d < D; ++d) {
+        const float kv = kT[d * kKT + st];
+#pragma unroll
+        for (int i = 0; i < kRowTile / 4; ++i) {
+          const int r = sr0 + 4 * i;
+          if (r < nr) acc[i] = fmaf(qs[r][d], kv, acc[i]);
+        }
+      }
+    } else if (valid) {
       const TR* kr = rk + t * tstride + (int64_t)h * D;
       for (int d = 0; d < D; ++d) {
         const float kv = Num<TR>::to_f(kr[d]);
@@ -286,7 +314,26 @@ __global__ __launch_bounds__(kAttnThreads) void attn_recent_kernel(smaq_attn_par
       const int r = pr0 + i * prs;
       if (i * prs < kRowTile && r < nr && pr0 < prs) o[i] *= alpha_s[r];
     }
-    if (pr0 < prs) {
+    if (staged) {
+      // the chunk's values, laid over the keys' stage ([token][dim]): all of
+      // a thread's loads are issued before the first use (one memory round
+      // trip, not one per token)
+      const int per = kAttnThreads / D, d = tid % D;
+      const TR* vc = rv + c0 * tstride + (int64_t)h * D + d;
+#pragma unroll 8
+      for (int tk = tid / D; tk < nt; tk += per) kT[tk * D + d] = Num<TR>::to_f(vc[tk * tstride]);
+      __syncthreads();
+      if (pr0 < prs) {
+        for (int k = 0; k < nt; ++k) {
+          const float vv = kT[k * D + pd];
+#pragma unroll
+          for (int i = 0; i < kRowTile; ++i) {
+            const int r = pr0 + i * prs;
+            if (i * prs < kRowTile && r < nr) o[i] = fmaf(sc[r][k], vv, o[i]);
+          }
+        }
+      }
+    } else if (pr0 < prs) {
       for (int k = 0; k < nt; ++k) {
         const float vv = Num<TR>::to_f(rv[(c0 + k) * tstride + (int64_t)h * D + pd]);
 #pragma unroll
@@ -537,7 +584,25 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
   // merges its several splits itself (its last workgroup per sequence and KV
   // head): no combine launch.
   const bool direct = pl.mfma && pl.s_hist == 1 && pl.s_recent == 0;
-  const bool merge = pl.mfma && pl.s_hist > 1 && pl.s_recent == 0 && p.arrivals != nullptr;
+  // With a recent part the decode kernel merges the recent window's partials
+  // too; the recent phase then runs first, in the same call.
+  const bool merge = pl.mfma && !direct && p.arrivals != nullptr && (pl.s_recent == 0 || (phases & 3) == 3);
+  auto launch_recent = [&]() -> int {
+    if (recent_decode_supported(p)) return launch_recent_decode(p, part, pl.s_hist, pl.s_recent, pl.recent_split, st);
+    dim3 grid(pl.s_recent, p.n_kv_heads * pl.row_tiles, p.batch);
+    switch (p.recent_dtype) {
+      case SMAQ_F32: hipLaunchKernelGGL(attn_recent_kernel<float>, grid, dim3(kAttnThreads), 0, st, p, part, pl.s_hist, pl.recent_split, pl.row_tiles); break;
+      case SMAQ_F16: hipLaunchKernelGGL(attn_recent_kernel<_Float16>, grid, dim3(kAttnThreads), 0, st, p, part, pl.s_hist, pl.recent_split, pl.row_tiles); break;
+      case SMAQ_BF16: hipLaunchKernelGGL(attn_recent_kernel<bf16>, grid, dim3(kAttnThreads), 0, st, p, part, pl.s_hist, pl.recent_split, pl.row_tiles); break;
+      default: set_error("smaq_attn_hybrid: unsupported recent dtype %d", p.recent_dtype); return SMAQ_EUNSUPPORTED;
+    }
+    return launch_status("smaq_attn_hybrid(recent)");
+  };
+  const bool recent_first = merge && pl.s_recent > 0;
+  if (recent_first) {
+    const int rc = launch_recent();
+    if (rc != SMAQ_OK) return rc;
+  }
   // The query rotation (given rot_mt) is one launch into q_hist ahead of
   // the history phase.
   if (p.has_history && p.rot_mt && (phases & 1)) {
@@ -595,15 +660,8 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
     if (rc != SMAQ_OK) return rc;
     if (!pl.mfma && (rc = launch_status("smaq_attn_hybrid(history)")) != SMAQ_OK) return rc;
   }
-  if (!pl.prefill && pl.s_recent > 0 && (phases & 2)) {
-    dim3 grid(pl.s_recent, p.n_kv_heads * pl.row_tiles, p.batch);
-    switch (p.recent_dtype) {
-      case SMAQ_F32: hipLaunchKernelGGL(attn_recent_kernel<float>, grid, dim3(kAttnThreads), 0, st, p, part, pl.s_hist, pl.recent_split, pl.row_tiles); break;
-      case SMAQ_F16: hipLaunchKernelGGL(attn_recent_kernel<_Float16>, grid, dim3(kAttnThreads), 0, st, p, part, pl.s_hist, pl.recent_split, pl.row_tiles); break;
-      case SMAQ_BF16: hipLaunchKernelGGL(attn_recent_kernel<bf16>, grid, dim3(kAttnThreads), 0, st, p, part, pl.s_hist, pl.recent_split, pl.row_tiles); break;
-      default: set_error("smaq_attn_hybrid: unsupported recent dtype %d", p.recent_dtype); return SMAQ_EUNSUPPORTED;
-    }
-    const int rc = launch_status("smaq_attn_hybrid(recent)");
+  if (!pl.prefill && !recent_first && pl.s_recent > 0 && (phases & 2)) {
+    const int rc = launch_recent();
     if (rc != SMAQ_OK) return rc;
   }
   if (!(phases & 4) || direct || merge) return SMAQ_OK;

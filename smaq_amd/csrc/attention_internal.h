@@ -76,6 +76,14 @@ int launch_prefill_planes_recent(const smaq_attn_params& p, const PrefillPlanes&
 int launch_prefill_mfma(const smaq_attn_params& p, const PrefillPart& pp, int n_splits, const Partials& part,
                         hipStream_t st);
 
+// Recent window of a decode step (attention_recent.hip): one query token per
+// sequence, head_dim 128, 1/2/4 query heads per KV head; impl 1 keeps the
+// generic kernel.  Writes the same partials as the generic recent kernel
+// (splits s_base .. s_base+n_splits-1).
+bool recent_decode_supported(const smaq_attn_params& p);
+int launch_recent_decode(const smaq_attn_params& p, const Partials& part, int s_base, int n_splits,
+                         int64_t split_len, hipStream_t st);
+
 // MFMA decode path (attention_mfma.hip).  Returns true when it can serve
 // these parameters (history only, decode shape, supported formats).
 bool mfma_decode_supported(const smaq_attn_params& p);

@@ -74,8 +74,9 @@ struct SplitRule {
   int slots;  // round-slots per CU (at most kMaxSlots)
   int tilt;   // weight step per slot; tilt * (slots - 1) < kSplitWeight
   int direct; // one split and no recent part: write the final output
-  int merge;  // several splits, no recent part, arrival counters given: the
-              // last workgroup of each (sequence, KV head) writes the output
+  int merge;  // arrival counters given (several splits, or a recent part
+              // whose partials an earlier launch wrote): the last workgroup
+              // of each (sequence, KV head) merges and writes the output
 };
 constexpr int kSplitWeight = 64;
 
@@ -294,6 +295,15 @@ __device__ __forceinline__ void store_out2(const smaq_attn_params& p, int64_t oi
       o[0] = Num<bf16>::from_f(o0);
       o[1] = Num<bf16>::from_f(o1);
     } break;
+  }
+}
+
+// x rounded to the output dtype (kept in fp32).
+__device__ __forceinline__ float round_out(const smaq_attn_params& p, float x) {
+  switch (p.out_dtype) {
+    case SMAQ_F32: return x;
+    case SMAQ_F16: return Num<_Float16>::round(x);
+    default: return Num<bf16>::round(x);
   }
 }
 
@@ -1004,7 +1014,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
   for (int i = tid; i < Q * 64; i += 256) {
     const int j = i >> 6, d = 2 * (i & 63);
     const int64_t base = part.idx(b, h, p.n_kv_heads, Q, j, 0);
-    float M = -__builtin_inff(), L = 0.0f, o0 = 0.0f, o1 = 0.0f;
+    // history splits [0, n_splits) sum into o, the recent window's splits
+    // (written by the recent launch before this kernel) into r
+    float M = -__builtin_inff(), L = 0.0f, o0 = 0.0f, o1 = 0.0f, r0 = 0.0f, r1 = 0.0f;
     for (int c0 = 0; c0 < S; c0 += 8) {
       // a chunk's loads are all issued before any is used
       float mv[8], lv[8];
@@ -1029,6 +1041,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
         L *= c;
         o0 *= c;
         o1 *= c;
+        r0 *= c;
+        r1 *= c;
         M = Mc;
       }
 #pragma unroll
@@ -1036,12 +1050,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
         if (!(lv[k] > 0.0f)) continue;
         const float wk = __expf(mv[k] - M);
         L = fmaf(lv[k], wk, L);
-        o0 += ov[k][0] * wk;
-        o1 += ov[k][1] * wk;
+        const float v0 = ov[k][0] * wk, v1 = ov[k][1] * wk;
+        if (c0 + k < rule.n_splits) {
+          o0 += v0;
+          o1 += v1;
+        } else {
+          r0 += v0;
+          r1 += v1;
+        }
       }
     }
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    store_out2(p, (qrow0 + j) * 128 + d, o0 * inv, o1 * inv);
+    o0 *= inv;
+    o1 *= inv;
+    if (S > rule.n_splits) {
+      // history and recent outputs each in the output dtype, then added (the
+      // combine kernel's order, as compute_hybrid_attention adds them)
+      o0 = round_out(p, round_out(p, o0) + round_out(p, r0 * inv));
+      o1 = round_out(p, round_out(p, o1) + round_out(p, r1 * inv));
+    }
+    store_out2(p, (qrow0 + j) * 128 + d, o0, o1);
   }
 }
 
@@ -1164,6 +1192,7 @@ int launch_mfma_decode(const smaq_attn_params& p, const HistAddr& a, const Parti
   rule.tilt = wide ? 0 : kSplitTilt4;
   rule.direct = direct && n_splits == 1 ? 1 : 0;
   rule.merge = merge && !rule.direct && p.arrivals ? 1 : 0;
+  SMAQ_REQUIRE(!rule.merge || part.S >= n_splits, "smaq_attn_hybrid: merge partials missing");
   if (p.key_bits == 3) launch_n<3>(p, a, part, rule, n_splits, order, st);
   else launch_n<4>(p, a, part, rule, n_splits, order, st);
   return launch_status("smaq_attn_hybrid(mfma decode)");

@@ -1,0 +1,222 @@
+// Exact recent window of a decode step (one query token per sequence,
+// head_dim 128, 1, 2 or 4 query heads per KV head): the partials of the
+// window's tokens for one (split, KV head, sequence), as the generic recent
+// kernel in attention.hip writes them, from wide coalesced loads.
+//
+// Reference: the recent segment of compute_hybrid_attention
+// (smaq/score.py:61-72): scores q . k * scale in fp32 against the exact keys,
+// one softmax shared with the history, the weights applied to the exact
+// values.  Here: per 64-token chunk, wave w takes tokens 16w..16w+15; a lane
+// holds a quarter of one token's key (32 dims, 16-byte loads: 4 lanes read a
+// 256-byte key row) and the same quarter of the G query rows in registers,
+// and the quarters are summed with two lane exchanges.  The online softmax
+// runs over the chunk (natural-log units, as the other partial writers); for
+// the weighted values lane l holds dims 2l, 2l+1 of its wave's 16 tokens (one
+// 256-byte value row per wave load).  The chunk's key and value loads are all
+// issued before any is used, so a chunk costs one memory round trip.
+#include <math.h>
+
+#include "attention_internal.h"
+
+namespace smaq {
+
+namespace {
+
+constexpr int kRD = 128;     // head_dim
+constexpr int kRChunk = 64;  // tokens per online-softmax step (16 per wave)
+
+// Eight consecutive recent-window elements (16 or 32 bytes) -> fp32.
+template <typename T>
+__device__ __forceinline__ void load8(const T* src, float* out) {
+  if constexpr (sizeof(T) == 2) {
+    const uint4 v = *(const uint4*)src;
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[2 * i] = Num<T>::to_f(__builtin_bit_cast(T, (uint16_t)w[i]));
+      out[2 * i + 1] = Num<T>::to_f(__builtin_bit_cast(T, (uint16_t)(w[i] >> 16)));
+    }
+  } else {
+    const float4 a = *(const float4*)src, c = *(const float4*)(src + 4);
+    out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+    out[4] = c.x; out[5] = c.y; out[6] = c.z; out[7] = c.w;
+  }
+}
+
+// Two consecutive elements, kept as loaded (one or two dwords).
+template <typename T>
+struct Pair {
+  uint32_t w[sizeof(T) == 2 ? 1 : 2];
+  __device__ __forceinline__ void load(const T* src) {
+    if constexpr (sizeof(T) == 2) {
+      w[0] = *(const uint32_t*)src;
+    } else {
+      const uint2 v = *(const uint2*)src;
+      w[0] = v.x; w[1] = v.y;
+    }
+  }
+  __device__ __forceinline__ float get(int i) const {
+    if constexpr (sizeof(T) == 2)
+      return Num<T>::to_f(__builtin_bit_cast(T, (uint16_t)(w[0] >> (16 * i))));
+    else
+      return __builtin_bit_cast(float, w[i]);
+  }
+};
+
+template <typename TR, int G>
+__global__ __launch_bounds__(256) void recent_decode_kernel(smaq_attn_params p, Partials part, int s_base,
+                                                            int64_t split_len) {
+  __shared__ float sc[G][kRChunk];     // the chunk's scores, then weights
+  __shared__ float m_s[G], l_s[G], a_s[G];
+  __shared__ float red[4][G][kRD];     // per-wave outputs, summed at the end
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int64_t len = p.recent_len ? min((int64_t)p.recent_len[b], (int64_t)p.max_recent_len) : p.max_recent_len;
+  const int64_t t0 = (int64_t)s * split_len;
+  const int64_t t1 = min(len, t0 + split_len);
+  const int64_t tstride = (int64_t)p.n_kv_heads * kRD;
+  const TR* rk = (const TR*)p.recent_k + (int64_t)b * p.recent_batch_stride + (int64_t)h * kRD;
+  const TR* rv = (const TR*)p.recent_v + (int64_t)b * p.recent_batch_stride + (int64_t)h * kRD;
+  const long long qpos = p.q_positions ? p.q_positions[b] : 0;
+
+  // this lane's quarter (dims 32 dq ..) of the G query rows
+  const int tq = lane & 15, dq = lane >> 4;
+  float q[G][32];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float* qr = p.q_exact + ((int64_t)b * p.n_q_heads + h * G + g) * kRD + 32 * dq;
+#pragma unroll
+    for (int i = 0; i < 32; i += 4) {
+      const float4 v = *(const float4*)(qr + i);
+      q[g][i] = v.x; q[g][i + 1] = v.y; q[g][i + 2] = v.z; q[g][i + 3] = v.w;
+    }
+  }
+  if (tid < G) {
+    m_s[tid] = -__builtin_inff();
+    l_s[tid] = 0.0f;
+  }
+  float o[G][2];
+#pragma unroll
+  for (int g = 0; g < G; ++g) o[g][0] = o[g][1] = 0.0f;
+  __syncthreads();
+
+  for (int64_t c0 = t0; c0 < t1; c0 += kRChunk) {
+    const int nt = (int)min((int64_t)kRChunk, t1 - c0);
+    // loads: this lane's key quarter (token 16w + tq) and its wave's 16 value
+    // pairs; rows past the window read its last token and are dropped
+    const int kt = 16 * w + tq;
+    float k[32];
+    {
+      const TR* kr = rk + (c0 + min(kt, nt - 1)) * tstride + 32 * dq;
+#pragma unroll
+      for (int i = 0; i < 32; i += 8) load8(kr + i, k + i);
+    }
+    Pair<TR> v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i].load(rv + (c0 + min(16 * w + i, nt - 1)) * tstride + 2 * lane);
+    // scores: quarter dot products, summed over the 4 lanes of a token
+    float acc[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      acc[g] = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) acc[g] = fmaf(q[g][i], k[i], acc[g]);
+      acc[g] += __shfl_xor(acc[g], 16, 64);
+      acc[g] += __shfl_xor(acc[g], 32, 64);
+    }
+    if (dq == 0) {
+      const bool live = kt < nt && !(p.q_positions && p.recent_pos_offset + c0 + kt > qpos);
+#pragma unroll
+      for (int g = 0; g < G; ++g) sc[g][kt] = live ? acc[g] * p.scale : -__builtin_inff();
+    }
+    __syncthreads();
+    // online softmax of row g by wave g
+    if (w < G) {
+      const float x = sc[w][lane];
+      const float m_old = m_s[w];
+      const float m_new = fmaxf(m_old, warp_max(x));
+      const float pw = m_new == -__builtin_inff() ? 0.0f : __expf(x - m_new);
+      const float alpha = m_old == -__builtin_inff() ? 0.0f : __expf(m_old - m_new);
+      const float ls = warp_sum(pw);
+      sc[w][lane] = pw;
+      if (lane == 0) {
+        l_s[w] = l_s[w] * alpha + ls;
+        m_s[w] = m_new;
+        a_s[w] = alpha;
+      }
+    }
+    __syncthreads();
+    // weighted values of this wave's tokens
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float alpha = a_s[g];
+      o[g][0] *= alpha;
+      o[g][1] *= alpha;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (16 * w + i >= nt) break;  // uniform over the wave
+      const float v0 = v[i].get(0), v1 = v[i].get(1);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float pw = sc[g][16 * w + i];
+        o[g][0] = fmaf(pw, v0, o[g][0]);
+        o[g][1] = fmaf(pw, v1, o[g][1]);
+      }
+    }
+    __syncthreads();  // sc is rewritten by the next chunk
+  }
+
+  // the 4 waves' sums, then the partial of each query row
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    red[w][g][2 * lane] = o[g][0];
+    red[w][g][2 * lane + 1] = o[g][1];
+  }
+  __syncthreads();
+  for (int i = tid; i < G * kRD; i += 256) {
+    const int g = i / kRD, d = i - g * kRD;
+    const float sum = (red[0][g][d] + red[1][g][d]) + (red[2][g][d] + red[3][g][d]);
+    const int64_t pi = part.idx(b, h, p.n_kv_heads, G, g, s_base + s);
+    part.o[pi * kRD + d] = sum;
+    if (d == 0) {
+      part.m[pi] = m_s[g];
+      part.l[pi] = l_s[g];
+    }
+  }
+}
+
+template <typename TR>
+void launch_g(const smaq_attn_params& p, const Partials& part, int s_base, int n_splits, int64_t split_len,
+              hipStream_t st) {
+  const dim3 grid((unsigned)n_splits, (unsigned)p.n_kv_heads, (unsigned)p.batch);
+  switch (p.n_q_heads / p.n_kv_heads) {
+    case 1: hipLaunchKernelGGL((recent_decode_kernel<TR, 1>), grid, dim3(256), 0, st, p, part, s_base, split_len); break;
+    case 2: hipLaunchKernelGGL((recent_decode_kernel<TR, 2>), grid, dim3(256), 0, st, p, part, s_base, split_len); break;
+    default: hipLaunchKernelGGL((recent_decode_kernel<TR, 4>), grid, dim3(256), 0, st, p, part, s_base, split_len); break;
+  }
+}
+
+}  // namespace
+
+bool recent_decode_supported(const smaq_attn_params& p) {
+  const int g = p.n_q_heads / p.n_kv_heads;
+  return p.impl != 1 && p.has_recent && p.q_len == 1 && p.head_dim == kRD && (g == 1 || g == 2 || g == 4) &&
+         (p.recent_dtype == SMAQ_F32 || p.recent_dtype == SMAQ_F16 || p.recent_dtype == SMAQ_BF16) &&
+         // 16-byte key loads and 4- or 8-byte value loads at element offsets
+         // that are multiples of 8 and 2
+         (((uintptr_t)p.recent_k | (uintptr_t)p.recent_v) & 15) == 0 && ((uintptr_t)p.q_exact & 15) == 0;
+}
+
+int launch_recent_decode(const smaq_attn_params& p, const Partials& part, int s_base, int n_splits,
+                         int64_t split_len, hipStream_t st) {
+  switch (p.recent_dtype) {
+    case SMAQ_F32: launch_g<float>(p, part, s_base, n_splits, split_len, st); break;
+    case SMAQ_F16: launch_g<_Float16>(p, part, s_base, n_splits, split_len, st); break;
+    default: launch_g<bf16>(p, part, s_base, n_splits, split_len, st); break;
+  }
+  return launch_status("smaq_attn_hybrid(recent decode)");
+}
+
+}  // namespace smaq

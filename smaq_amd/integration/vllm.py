@@ -35,6 +35,7 @@ from __future__ import annotations
 import logging
 import math
 import types
+from collections import OrderedDict
 from dataclasses import dataclass, field
 from typing import Optional
 
@@ -99,12 +100,16 @@ class PagedLayerCache:
     allocated on the first write, from the size of vLLM's cache tensor.
     """
 
+    # decode plans kept per layer (least recently used dropped first)
+    MAX_PLANS = 8
+
     def __init__(self, store: CompressedKVStore):
         self.store = store           # supplies the key strategy and value format
         self.num_blocks = 0
         self.block_size = 0
         self.pools: Optional[dict[str, torch.Tensor]] = None
         self.tokens_written = 0
+        self._plans: "OrderedDict[tuple, object]" = OrderedDict()
 
     @staticmethod
     def cache_geometry(kv_cache: torch.Tensor, num_kv_heads: int, head_dim: int) -> tuple[int, int]:
@@ -172,28 +177,61 @@ class PagedLayerCache:
             return 0
         return sum(t.numel() * t.element_size() for t in self.pools.values())
 
-    def decode(self, query: torch.Tensor, block_table: torch.Tensor, seq_lens: torch.Tensor, max_seq_len: int,
-               num_query_heads: int, scale: float, out: torch.Tensor) -> None:
-        """One decode token per sequence: query [B, Hq, D] over each
-        sequence's ``seq_lens[b]`` tokens through its block table; the result
-        is written to out [B, Hq, D] (out's dtype)."""
+    @staticmethod
+    def length_bucket(max_seq_len: int) -> int:
+        """The plan's length bound for a step whose longest sequence has
+        max_seq_len tokens: the next power of two (at least 16), so that a
+        growing batch re-uses one plan per doubling of its longest context."""
+        return max(16, 1 << (max(int(max_seq_len), 1) - 1).bit_length())
+
+    def _plan(self, query: torch.Tensor, block_table: torch.Tensor, max_seq_len: int, num_query_heads: int,
+              scale: float, out_dtype: torch.dtype):
+        """The cached decode plan for this batch shape (built on first use)."""
         from smaq_amd.score import AttentionPlan
         st = self.store
         B = query.shape[0]
-        fused = st.key_strategy.fused_history()
+        bound = self.length_bucket(max_seq_len)
+        key = (B, int(block_table.shape[1]), num_query_heads, float(scale), out_dtype, query.dtype, bound,
+               query.device)
+        plan = self._plans.get(key)
+        if plan is not None:
+            self._plans.move_to_end(key)
+            return plan
         pools = self.pools
         plan = AttentionPlan(
-            query=query.reshape(B, 1, num_query_heads, st.head_dim), fused=fused,
+            query=query.reshape(B, 1, num_query_heads, st.head_dim), fused=st.key_strategy.fused_history(),
             key_codes=pools["k_codes"], key_norms=pools.get("k_norms"), val_data=pools["v_data"],
             val_scales=pools["v_scales"], val_zeros=pools["v_zeros"], val_bits=st.value_bits,
             val_group=st.value_group_size, n_kv_heads=st.num_kv_heads,
-            hist_len=seq_lens[:B].to(query.device, torch.int64), max_hist_len=int(max_seq_len),
-            block_table=block_table[:B], block_size=self.block_size, scale=scale, out_dtype=out.dtype)
-        res = plan.run(query.reshape(B, 1, num_query_heads, st.head_dim))
-        out.copy_(res.reshape(out.shape))
+            hist_len=torch.zeros(B, dtype=torch.int64, device=query.device), max_hist_len=bound,
+            block_table=block_table[:B], block_size=self.block_size, scale=scale, out_dtype=out_dtype)
+        self._plans[key] = plan
+        while len(self._plans) > self.MAX_PLANS:
+            self._plans.popitem(last=False)
+        return plan
+
+    def decode(self, query: torch.Tensor, block_table: torch.Tensor, seq_lens: torch.Tensor, max_seq_len: int,
+               num_query_heads: int, scale: float, out: torch.Tensor) -> None:
+        """One decode token per sequence: query [B, Hq, D] over each
+        sequence's ``seq_lens[b]`` tokens (``max_seq_len`` >= every one of
+        them) through its block table; the result is written to out
+        [B, Hq, D] (out's dtype).  The launch is prepared once per batch
+        shape and re-used: a step copies the lengths into the plan, points it
+        at the block table and writes straight into ``out`` when out is
+        contiguous."""
+        B = query.shape[0]
+        plan = self._plan(query, block_table, max_seq_len, num_query_heads, scale, out.dtype)
+        plan.set_lengths(hist_len=seq_lens)
+        plan.set_block_table(block_table)
+        q = query.reshape(B, 1, num_query_heads, self.store.head_dim)
+        if out.is_contiguous():
+            plan.run_into(q, out)
+        else:
+            out.copy_(plan.run(q).reshape(out.shape))
 
     def reset(self) -> None:
         self.tokens_written = 0
+        self._plans.clear()
 
 
 @dataclass
@@ -205,6 +243,9 @@ class LayerState:
     engine: KVCaptureEngine
     _log_count: int = 0
     paged: Optional[PagedLayerCache] = None
+    # decode plan of the reference layout and what it was built for
+    ref_plan: Optional[object] = None
+    ref_plan_key: Optional[tuple] = None
 
     @property
     def supports_hybrid(self) -> bool:
@@ -214,6 +255,7 @@ class LayerState:
         self.engine.reset()
         if self.paged is not None:
             self.paged.reset()
+        self.ref_plan = self.ref_plan_key = None
         self._log_count = 0
 
 
@@ -341,6 +383,47 @@ def _paged_decode(state: LayerState, self_impl, query, attn_metadata, output):
     return _deliver(res, query, output, n, cfg)
 
 
+def _reference_layout_decode(state: LayerState, self_impl, q: torch.Tensor, flat, query, output):
+    """The reference layout's decode step (one store per layer, the exact
+    ring as the recent window: smaq/integration/vllm.py:224-255) through a
+    plan kept on the layer.  The plan is rebuilt only when the history
+    changes (a ring spill, or its columns growing) or the step's shape does;
+    otherwise a step sets the ring's fill and launches, writing straight into
+    ``output`` when it is a contiguous buffer of the query's dtype.  None
+    when the store has no fused kernel description or the ring is empty (the
+    caller then takes the one-shot path)."""
+    from smaq_amd.score import AttentionPlan, _flat_tensors
+    cfg, store, ring = state.config, state.store, state.engine.ring
+    fh = getattr(store.quantizer, "fused_history", None)
+    fused = fh() if fh is not None else None
+    fill = ring.size
+    if fused is None or fill == 0:
+        return None
+    n = q.shape[0]
+    scale = getattr(self_impl, "scale", None)
+    scale = 1.0 / math.sqrt(cfg.head_dim) if scale is None else float(scale)
+    (codes, norms, vdata, vsc, vz), stride = _flat_tensors(flat)
+    hist = (codes, norms, vdata, vsc, vz)
+    key = (n, q.dtype, q.device, scale, flat.num_tokens, stride,
+           tuple(0 if t is None else t.data_ptr() for t in hist), ring._slots_k.data_ptr(), ring.capacity)
+    if state.ref_plan_key != key:
+        state.ref_plan = AttentionPlan(
+            query=q.unsqueeze(0), fused=fused, key_codes=codes, key_norms=norms, val_data=vdata, val_scales=vsc,
+            val_zeros=vz, val_bits=store.value_bits, val_group=store.value_group_size, n_kv_heads=store.num_kv_heads,
+            hist_len=None, max_hist_len=flat.num_tokens, hist_head_stride=stride,
+            recent_k=ring._slots_k.unsqueeze(0), recent_v=ring._slots_v.unsqueeze(0),
+            recent_len=torch.full((1,), fill, dtype=torch.int64, device=q.device), max_recent_len=ring.capacity,
+            scale=scale, out_dtype=q.dtype, recent_pos_offset=flat.num_tokens)
+        state.ref_plan_key = key
+    else:
+        state.ref_plan.set_lengths(recent_len=fill)
+    plan = state.ref_plan
+    if output is not None and output.dtype == q.dtype and output[:n].is_contiguous():
+        plan.run_into(q.unsqueeze(0), output[:n])
+        return output
+    return _deliver(plan.run(q.unsqueeze(0)).squeeze(0), query, output, n, cfg)
+
+
 def _make_patched_forward(orig_fn, state: LayerState, no_alloc: bool = False, capture_in_forward: bool = False):
     """Attention forward with SMAQ serving (smaq/integration/vllm.py:166-272)."""
 
@@ -381,6 +464,9 @@ def _make_patched_forward(orig_fn, state: LayerState, no_alloc: bool = False, ca
                     q = query[:n]
                     if q.dim() == 2:
                         q = q.view(n, cfg.num_query_heads, cfg.head_dim)
+                    res = _reference_layout_decode(state, self_impl, q, flat, query, output)
+                    if res is not None:
+                        return res
                     recent = state.engine.ring.peek()
                     res = compute_hybrid_attention(query=q, store=state.store,
                                                    recent_k=recent[0] if recent else None,

@@ -42,6 +42,12 @@ def _per_sequence_index(t: Optional[torch.Tensor], batch: int, dev: torch.device
     return t[:batch].to(dev, torch.int64).contiguous()
 
 
+def _own_copy(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+    """A private copy of a per-sequence index tensor: the plan's buffer,
+    updated in place on re-use, never the caller's tensor."""
+    return None if t is None else t.clone()
+
+
 class AttentionPlan:
     """A prepared fused-attention launch.
 
@@ -108,6 +114,9 @@ class AttentionPlan:
         self.q_hist = None
         self.rot_t = None
         self._q_raw = None
+        self.hist_len = None        # the plan's own per-sequence length buffers
+        self.recent_len = None      # (int64; updated in place by set_lengths)
+        self._block_table = None
         if has_hist:
             if fused.rot_t is not None:
                 # The library rotates the raw query itself (inside the decode
@@ -146,8 +155,9 @@ class AttentionPlan:
             p.val_bits, p.val_group = val_bits, val_group
             p.val_scales, p.val_zeros = val_scales.data_ptr(), val_zeros.data_ptr()
             p.val_dtype = _native.dtype_code(val_scales.dtype)
-            hist_len = _per_sequence_index(hist_len, B, dev, "hist_len")
+            hist_len = _own_copy(_per_sequence_index(hist_len, B, dev, "hist_len"))
             hist_seq_start = _per_sequence_index(hist_seq_start, B, dev, "hist_seq_start")
+            self.hist_len = hist_len
             p.hist_len = None if hist_len is None else hist_len.data_ptr()
             p.hist_seq_start = None if hist_seq_start is None else hist_seq_start.data_ptr()
             p.hist_head_stride = int(hist_head_stride)
@@ -156,7 +166,7 @@ class AttentionPlan:
                     raise ValueError(f"block_table must be an integer [>= {B}, max_blocks] tensor, "
                                      f"got {tuple(block_table.shape)} {block_table.dtype}")
                 bt = block_table[:B].to(dev, torch.int32).contiguous()
-                keep.append(bt)
+                self._block_table = bt
                 p.block_table = bt.data_ptr()
                 p.max_blocks = bt.shape[-1]
                 p.block_size = int(block_size)
@@ -165,8 +175,9 @@ class AttentionPlan:
                      if t is not None]
         if has_recent:
             rk, rv = recent_k.contiguous(), recent_v.contiguous()
-            recent_len = _per_sequence_index(recent_len, B, dev, "recent_len")
-            keep += [rk, rv] + ([recent_len] if recent_len is not None else [])
+            recent_len = _own_copy(_per_sequence_index(recent_len, B, dev, "recent_len"))
+            self.recent_len = recent_len
+            keep += [rk, rv]
             p.has_recent = 1
             p.recent_k, p.recent_v = rk.data_ptr(), rv.data_ptr()
             p.recent_dtype = _native.dtype_code(rk.dtype)
@@ -214,6 +225,58 @@ class AttentionPlan:
     def run(self, query: torch.Tensor) -> torch.Tensor:
         self.load_query(query)
         return self.launch()
+
+    # -- re-use across steps: a serving loop keeps one plan per batch shape
+    # and rebinds what changes from step to step (lengths, block table,
+    # output), so a step allocates nothing and costs its launches only.
+
+    def set_lengths(self, hist_len=None, recent_len=None) -> None:
+        """Copy new per-sequence lengths (an integer tensor with >= B entries,
+        or one int for every sequence) into the plan's own buffers; the plan
+        must have been built with lengths of that kind.  Lengths above the
+        plan's maxima are clamped by the kernels."""
+        B = self.shape[0]
+        for new, own, what in ((hist_len, self.hist_len, "hist_len"), (recent_len, self.recent_len, "recent_len")):
+            if new is None:
+                continue
+            if own is None:
+                raise ValueError(f"plan was built without per-sequence {what}")
+            if isinstance(new, int):
+                own.fill_(new)
+                continue
+            if new.dtype.is_floating_point or new.dtype == torch.bool or new.reshape(-1).numel() < B:
+                raise ValueError(f"{what} must be an integer tensor with >= {B} entries")
+            own.copy_(new.reshape(-1)[:B])
+
+    def set_block_table(self, block_table: torch.Tensor) -> None:
+        """Point the plan at a block table of the shape it was built with
+        ([>= B, max_blocks] integer; copied only if not int32, contiguous and
+        on the plan's device)."""
+        if self._block_table is None:
+            raise ValueError("plan was built without a block table")
+        B, mb = self._block_table.shape
+        if block_table.dim() != 2 or block_table.shape[0] < B or block_table.shape[1] != mb \
+                or block_table.dtype.is_floating_point:
+            raise ValueError(f"block_table must be an integer [>= {B}, {mb}] tensor, got "
+                             f"{tuple(block_table.shape)} {block_table.dtype}")
+        bt = block_table[:B].to(self.device, torch.int32).contiguous()
+        self._block_table = bt
+        self.params.block_table = bt.data_ptr()
+
+    def run_into(self, query: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+        """``run`` writing the result straight into ``out`` (contiguous, the
+        plan's output dtype and element count, on its device); returns out."""
+        if (out.dtype != self.out.dtype or out.numel() != self.out.numel() or not out.is_contiguous()
+                or out.device != self.device):
+            raise ValueError(f"out must be a contiguous {self.out.dtype} tensor of {self.out.numel()} elements "
+                             f"on {self.device}")
+        self.load_query(query)
+        self.params.out = out.data_ptr()
+        try:
+            _native.attn_hybrid(self.params, self.device)
+        finally:
+            self.params.out = self.out.data_ptr()
+        return out
 
 
 def launch_fused_attention(*, query: torch.Tensor, **kw) -> torch.Tensor:

@@ -253,3 +253,71 @@ def test_mfma_decode_split_merge(dev, qdtype):
     for b in (0, 2):
         assert_attn_close(out1[b:b + 1], _oracle(codec, keys[b], vals[b], q[b:b + 1], hkv * g, hkv),
                           f"split merge {qdtype} seq {b}")
+
+
+@pytest.mark.parametrize("odtype", [torch.float32, torch.bfloat16])
+def test_mfma_decode_merge_with_recent(dev, odtype):
+    """History in several splits plus an exact recent window (ragged lengths,
+    one sequence with an empty window): the recent phase runs first and the
+    decode kernel's last workgroup per unit merges history and recent
+    partials, rounding each to the output dtype before adding them.  Bit for
+    bit the separate launches (history, recent, combine phases), and the
+    oracle on sampled sequences."""
+    strat, codec = _codec_pair(dev, 3, 350)
+    hkv, g, RW = 8, 4, 40
+    lens = [3000, 5000, 700]
+    rl = [40, 0, 17]
+    gen = torch.Generator().manual_seed(351)
+    keys = [sample_keys(n * hkv, seed=352 + i).reshape(n, hkv, 128).bfloat16() for i, n in enumerate(lens)]
+    vals = [torch.randn(n, hkv, 128, generator=gen).bfloat16() for n in lens]
+    rk = torch.randn(len(lens), RW, hkv, 128, generator=gen).bfloat16()
+    rv = torch.randn(len(lens), RW, hkv, 128, generator=gen).bfloat16()
+    kvb = QuantizedKVBatch.encode(strat, [k.to(dev) for k in keys], [v.to(dev) for v in vals])
+    q = torch.randn(len(lens), hkv * g, 128, generator=gen).to(odtype)
+    qd = q.to(dev)
+    plan = kvb.plan(qd, recent_k=rk.to(dev), recent_v=rv.to(dev), recent_len=torch.tensor(rl), impl=2)
+    out = plan.run(qd).clone()
+    again = plan.run(qd).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(out, again) and int(plan.arrivals.abs().sum()) == 0
+    plan.out.zero_()
+    plan.load_query(qd)
+    for ph in (1, 2, 4):
+        plan.launch(phases=ph)
+    torch.cuda.synchronize()
+    assert torch.equal(plan.out, out), f"merge with recent differs: {(plan.out.float() - out.float()).abs().max()}"
+    for b in range(len(lens)):
+        st = R.Store(codec, 128, hkv)
+        st.append_chunk(keys[b], vals[b])
+        n = rl[b]
+        want = R.hybrid_attention(q[b:b + 1], st, rk[b, :n] if n else None, rv[b, :n] if n else None, hkv * g)
+        assert_attn_close(out[b:b + 1].squeeze(1), want, f"merge with recent {odtype} seq {b}")
+
+
+@pytest.mark.parametrize("g,rdtype", [(1, torch.float32), (2, torch.float16), (4, torch.bfloat16)])
+def test_recent_decode_kernel(dev, g, rdtype):
+    """The decode-shape recent-window kernel (one query token, head_dim 128,
+    1/2/4 query heads per KV head) over ragged windows of up to two 64-token
+    chunks (100, 1, 64, 65 and 0 tokens): every sequence matches the oracle,
+    and the generic kernels (impl 1) within the same tolerance."""
+    strat, codec = _codec_pair(dev, 3, 360 + g)
+    hkv, RW = 4, 100
+    lens = [500, 300, 64, 1000, 129]
+    rl = [100, 1, 64, 65, 0]
+    gen = torch.Generator().manual_seed(361 + g)
+    keys = [sample_keys(n * hkv, seed=362 + i).reshape(n, hkv, 128).bfloat16() for i, n in enumerate(lens)]
+    vals = [torch.randn(n, hkv, 128, generator=gen).bfloat16() for n in lens]
+    rk = (torch.randn(len(lens), RW, hkv, 128, generator=gen) * 0.5).to(rdtype)
+    rv = torch.randn(len(lens), RW, hkv, 128, generator=gen).to(rdtype)
+    kvb = QuantizedKVBatch.encode(strat, [k.to(dev) for k in keys], [v.to(dev) for v in vals])
+    q = torch.randn(len(lens), hkv * g, 128, generator=gen).bfloat16()
+    args = dict(recent_k=rk.to(dev), recent_v=rv.to(dev), recent_len=torch.tensor(rl))
+    out = kvb.attention(q.to(dev), **args)
+    gen_out = kvb.attention(q.to(dev), impl=1, **args)
+    for b in range(len(lens)):
+        st = R.Store(codec, 128, hkv)
+        st.append_chunk(keys[b], vals[b])
+        n = rl[b]
+        want = R.hybrid_attention(q[b:b + 1], st, rk[b, :n] if n else None, rv[b, :n] if n else None, hkv * g)
+        assert_attn_close(out[b:b + 1], want, f"recent kernel g={g} {rdtype} seq {b}")
+        assert_attn_close(gen_out[b:b + 1], want, f"generic recent g={g} {rdtype} seq {b}")

@@ -156,3 +156,77 @@ def test_paged_pools_batch_decode(dev):
     check(1)
     s = I.get_stats(runner)["l0"]
     assert s["compressed_tokens"] == sum(lens) + 2 * B and s["memory_bytes"] == st.paged.memory_bytes()
+
+
+def test_reference_layout_plan_reuse(dev):
+    """Decode steps of the reference layout re-use the layer's plan while the
+    history is unchanged (only the ring's fill moves) and rebuild it when a
+    spill grows the history; every step equals a one-shot
+    compute_hybrid_attention over the same store and ring bit for bit, and
+    is written straight into the output buffer."""
+    from smaq_amd.score import compute_hybrid_attention
+    hq, hkv, D, C = 8, 2, 128, 16
+    impl = FakeFlashImpl(hq, hkv, D)
+    kv = torch.zeros(2, 32, 16, hkv, D, dtype=torch.bfloat16, device=dev)
+    runner = make_runner({"l0": impl}, dev, {"l0": kv})
+    calib = {"l0": R.fit_sigma_centered(sample_keys(64, seed=171))}
+    st = I.install_hooks(runner, calibration_covariances=calib, key_bits=3, initial_layers_count=0,
+                         mode=V.MODE_CAPTURE_ONLY, ring_capacity=C)["l0"]
+    T = 200
+    k = sample_keys((T + 40) * hkv, seed=172).reshape(T + 40, hkv, D).bfloat16().to(dev)
+    v = torch.randn(T + 40, hkv, D, generator=torch.Generator().manual_seed(173)).bfloat16().to(dev)
+    impl.do_kv_cache_update(None, k[:T], v[:T], kv, torch.arange(T, device=dev))
+    V.set_mode(V.MODE_HYBRID)
+    plans, hist = [], []
+    for step in range(20):
+        t = T + step
+        impl.do_kv_cache_update(None, k[t:t + 1], v[t:t + 1], kv, torch.tensor([t], device=dev))
+        q = torch.randn(1, hq * D, generator=torch.Generator().manual_seed(180 + step)).bfloat16().to(dev)
+        out = torch.zeros(1, hq * D, dtype=torch.bfloat16, device=dev)
+        m = meta(1, 1, seq_lens=torch.tensor([t + 1], device=dev), block_table=torch.zeros(1, 32, dtype=torch.int32))
+        assert impl.forward(None, q, k[t:t + 1], v[t:t + 1], kv, m, output=out) is out
+        rk, rv = st.engine.ring.peek()
+        want = compute_hybrid_attention(q.view(1, hq, D), st.store, rk, rv, hq, scale=impl.scale)
+        assert torch.equal(out.view(1, hq, D), want), f"step {step}"
+        plans.append(st.ref_plan)
+        hist.append(st.store.num_tokens)
+    # one plan per history length (the ring spills every C tokens)
+    for a in range(1, len(plans)):
+        assert (plans[a] is plans[a - 1]) == (hist[a] == hist[a - 1]), a
+    assert len(set(hist)) >= 2 and len({id(p) for p in plans}) == len(set(hist))
+    assert impl.calls.count("forward") == 0
+
+
+def test_paged_plan_reuse(dev):
+    """Paged decode steps re-use one plan per batch shape and length bucket
+    (next power of two of the longest sequence): lengths move within the
+    bucket without a rebuild, a new bucket builds a second plan, and every
+    step matches a plan built for that step's exact lengths."""
+    from smaq_amd.batch import PagedQuantizedKV
+    hq, hkv, D, bs = 32, 8, 128, 16
+    B, nblk = 5, 200
+    st_ = I.install_hooks(make_runner({"l0": FakeFlashImpl(hq, hkv, D)}, dev,
+                                      {"l0": torch.zeros(2, nblk, bs, hkv, D, dtype=torch.bfloat16, device=dev)}),
+                          calibration_covariances={"l0": R.fit_sigma_centered(sample_keys(64, seed=191))},
+                          key_bits=3, initial_layers_count=0, mode=V.MODE_HYBRID, paged=True)["l0"]
+    pc = st_.paged
+    g = torch.Generator().manual_seed(192)
+    pc.ensure(nblk, bs, torch.bfloat16, torch.bfloat16, dev)
+    slots = torch.randperm(nblk * bs, generator=g)[: 600].to(dev)
+    keys = sample_keys(600 * hkv, seed=193).reshape(600, hkv, D).bfloat16().to(dev)
+    vals = torch.randn(600, hkv, D, generator=g).bfloat16().to(dev)
+    pc.write(keys, vals, slots)
+    table = torch.randint(0, nblk, (B, 40), generator=g, dtype=torch.int32).to(dev)
+    made = []
+    for step, lens in enumerate([[100, 300, 17, 250, 64], [101, 301, 18, 251, 65], [101, 520, 18, 251, 65]]):
+        q = torch.randn(B, hq, D, generator=torch.Generator().manual_seed(200 + step)).bfloat16().to(dev)
+        sl = torch.tensor(lens, dtype=torch.int32, device=dev)
+        out = torch.empty(B, hq, D, dtype=torch.bfloat16, device=dev)
+        pc.decode(q, table, sl, max(lens), hq, 1.0 / D ** 0.5, out)
+        made.append(len(pc._plans))
+        pools = {name: t.view(nblk, hkv, bs, *t.shape[1:]) for name, t in pc.pools.items()}
+        fresh = PagedQuantizedKV(st_.store.key_strategy, pools["k_codes"], pools["k_norms"], pools["v_data"],
+                                 pools["v_scales"], pools["v_zeros"], table, lens, bs, 2, 32)
+        want = fresh.attention(q, scale=1.0 / D ** 0.5)
+        assert_attn_close(out, want.cpu(), f"paged plan re-use step {step}")
+    assert made == [1, 1, 2]

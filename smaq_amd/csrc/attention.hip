@@ -384,6 +384,10 @@ __global__ __launch_bounds__(kMaxHeadDim * kCombineRows) void attn_combine_kerne
   // the sums.  With up to 8 splits this is the plain two-pass merge.
   float M = -__builtin_inff();
   float L = 0.0f, oh = 0.0f, orc = 0.0f;
+  // a partial whose sum is NaN holds a NaN score: the reference's softmax
+  // row is then NaN, so the output row is too (the merge below would
+  // otherwise drop that partial)
+  bool poisoned = false;
   for (int s0 = 0; s0 < part.S; s0 += 8) {
     float mv[8], lv[8], ov[8];
 #pragma unroll
@@ -399,8 +403,10 @@ __global__ __launch_bounds__(kMaxHeadDim * kCombineRows) void attn_combine_kerne
     }
     float Mc = M;
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < 8; ++i) {
       if (lv[i] > 0.0f) Mc = fmaxf(Mc, mv[i]);
+      poisoned |= lv[i] != lv[i];
+    }
     if (Mc > M) {
       const float c = __expf(M - Mc);
       L *= c;
@@ -423,6 +429,7 @@ __global__ __launch_bounds__(kMaxHeadDim * kCombineRows) void attn_combine_kerne
   float res;
   if (p.has_history && p.has_recent) res = Num<TO>::round(Num<TO>::round(oh) + Num<TO>::round(orc));
   else res = p.has_history ? oh : orc;
+  if (poisoned) res = __builtin_nanf("");
   const int t = r / g, j = r - t * g;
   ((TO*)p.out)[(((int64_t)b * p.q_len + t) * p.n_q_heads + h * g + j) * D + d] = Num<TO>::from_f(res);
 }

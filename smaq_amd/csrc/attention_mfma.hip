@@ -298,6 +298,13 @@ __device__ __forceinline__ void store_out2(const smaq_attn_params& p, int64_t oi
   }
 }
 
+// NaN test on the bits: this file is built with -fno-honor-nans, under
+// which a floating-point self-comparison folds to false.
+__device__ __forceinline__ bool is_nan_bits(float x) {
+  return (__builtin_bit_cast(uint32_t, x) & 0x7fffffffu) > 0x7f800000u;
+}
+constexpr float kQuietNaN = __builtin_bit_cast(float, 0x7fc00000u);
+
 // x rounded to the output dtype (kept in fp32).
 __device__ __forceinline__ float round_out(const smaq_attn_params& p, float x) {
   switch (p.out_dtype) {
@@ -955,19 +962,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
     for (int ww = 0; ww < kMWaves; ++ww) M = lw[ww] > 0.0f ? fmaxf(M, mw[ww]) : M;
     float L = 0.0f;
     f32x2 O = {0.0f, 0.0f};
+    bool poisoned = false;  // a NaN score reached some wave's sum
 #pragma unroll
     for (int ww = 0; ww < kMWaves; ++ww) {
       const bool live = lw[ww] > 0.0f;
+      poisoned |= is_nan_bits(lw[ww]);
       const float f = live ? exp2f(mw[ww] - M) : 0.0f;
       L = live ? fmaf(lw[ww], f, L) : L;
       O[0] = live ? fmaf(ow[ww][0], f, O[0]) : O[0];
       O[1] = live ? fmaf(ow[ww][1], f, O[1]) : O[1];
     }
+    // a NaN score makes the reference's softmax row NaN: the partial's sum
+    // carries it to the merge (which would otherwise drop the partial)
+    if (poisoned) L = kQuietNaN;
     if (rule.direct) {
       // the output itself: the split combine's arithmetic for one partial
       // (o * (1 / l), zero without tokens), in the output dtype
       const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-      store_out2(p, (qrow0 + j) * 128 + d, O[0] * inv, O[1] * inv);
+      const float r0 = poisoned ? kQuietNaN : O[0] * inv, r1 = poisoned ? kQuietNaN : O[1] * inv;
+      store_out2(p, (qrow0 + j) * 128 + d, r0, r1);
     } else {
       const int64_t pi = part.idx(b, h, p.n_kv_heads, Q, j, s);
       const float Mn = M == -__builtin_inff() ? M : M * 0.6931471805599453f;
@@ -1017,6 +1030,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
     // history splits [0, n_splits) sum into o, the recent window's splits
     // (written by the recent launch before this kernel) into r
     float M = -__builtin_inff(), L = 0.0f, o0 = 0.0f, o1 = 0.0f, r0 = 0.0f, r1 = 0.0f;
+    bool poisoned = false;  // a partial whose sum is NaN (a NaN score)
     for (int c0 = 0; c0 < S; c0 += 8) {
       // a chunk's loads are all issued before any is used
       float mv[8], lv[8];
@@ -1034,8 +1048,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
       }
       float Mc = M;
 #pragma unroll
-      for (int k = 0; k < 8; ++k)
+      for (int k = 0; k < 8; ++k) {
         if (lv[k] > 0.0f) Mc = fmaxf(Mc, mv[k]);
+        poisoned |= is_nan_bits(lv[k]);
+      }
       if (Mc > M) {
         const float c = __expf(M - Mc);
         L *= c;
@@ -1069,6 +1085,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
       o0 = round_out(p, round_out(p, o0) + round_out(p, r0 * inv));
       o1 = round_out(p, round_out(p, o1) + round_out(p, r1 * inv));
     }
+    if (poisoned) o0 = o1 = kQuietNaN;
     store_out2(p, (qrow0 + j) * 128 + d, o0, o1);
   }
 }

@@ -46,7 +46,9 @@ from smaq_amd.capture import KVCaptureEngine
 from smaq_amd.score import MIN_HISTORY_FOR_SMAQ, compute_hybrid_attention
 from smaq_amd.store import CompressedKVStore
 
-logger = logging.getLogger("smaq_amd.integration.vllm")
+# the reference's logger name (smaq/integration/vllm.py:25), so that a
+# deployment's logging configuration carries over
+logger = logging.getLogger("smaq.integration.vllm")
 
 MODE_OFF = "off"
 MODE_CAPTURE_ONLY = "capture_only"

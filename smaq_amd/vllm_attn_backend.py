@@ -24,7 +24,8 @@ from typing import Any, Callable, Optional
 
 import smaq_amd.integration.vllm as _adapter
 
-logger = logging.getLogger("smaq_amd.attn")
+# the reference's logger name (smaq/vllm_attn_backend.py:14)
+logger = logging.getLogger("smaq.attn")
 
 MODE_SHADOW = "shadow"
 MODE_ACCUMULATE = "accumulate"

@@ -321,3 +321,33 @@ def test_recent_decode_kernel(dev, g, rdtype):
         want = R.hybrid_attention(q[b:b + 1], st, rk[b, :n] if n else None, rv[b, :n] if n else None, hkv * g)
         assert_attn_close(out[b:b + 1], want, f"recent kernel g={g} {rdtype} seq {b}")
         assert_attn_close(gen_out[b:b + 1], want, f"generic recent g={g} {rdtype} seq {b}")
+
+
+@pytest.mark.parametrize("lens", [[3000, 2000], [400, 300]])
+def test_nan_key_norm_gives_nan_rows(dev, lens):
+    """A NaN key norm makes that token's scores NaN, and the reference's
+    softmax (smaq/score.py:61-72) returns NaN for every query row that
+    scores it.  The fused paths do the same -- matrix-core decode with the
+    in-kernel split merge, with the combine launch, with one split writing
+    the output directly ([400, 300]), and the generic kernels -- while every
+    other row keeps its bits."""
+    strat, _ = _codec_pair(dev, 3, 370)
+    hkv, g = 2, 4
+    gen = torch.Generator().manual_seed(371)
+    keys = [sample_keys(n * hkv, seed=372 + i).reshape(n, hkv, 128).bfloat16().to(dev) for i, n in enumerate(lens)]
+    vals = [torch.randn(n, hkv, 128, generator=gen).bfloat16().to(dev) for n in lens]
+    kvb = QuantizedKVBatch.encode(strat, keys, vals)
+    q = torch.randn(len(lens), hkv * g, 128, generator=gen).bfloat16().to(dev)
+    clean = {impl: kvb.attention(q, impl=impl).clone() for impl in (1, 2)}
+    kvb.norms[1, 123] = float("nan")                 # sequence 0, KV head 1, token 123
+    bad = torch.zeros(len(lens), hkv * g, dtype=torch.bool)
+    bad[0, g:2 * g] = True
+    for impl in (1, 2):
+        for merge in ((True, False) if impl == 2 else (True,)):
+            plan = kvb.plan(q, impl=impl)
+            if not merge:
+                plan.params.arrivals = None
+            out = plan.run(q).squeeze(1).cpu()
+            what = f"impl {impl} merge {merge}"
+            assert bool(torch.isnan(out[bad]).all()), what
+            assert bool(torch.equal(out[~bad], clean[impl].cpu()[~bad])), what

@@ -179,7 +179,7 @@ def test_mla_passthrough(caplog):
     mla = FakeMLAImpl()
     runner = make_runner({"mla": mla}, CPU)
     I.install_hooks(runner, mode=V.MODE_HYBRID)
-    with caplog.at_level(logging.INFO, logger="smaq_amd.integration.vllm"):
+    with caplog.at_level(logging.INFO, logger="smaq.integration.vllm"):
         mla.do_kv_cache_update(None, None, None, None, None, None)
         mla.do_kv_cache_update(None, None, None, None, None, None)
     assert mla.calls == ["mla_update", "mla_update"]
@@ -222,7 +222,7 @@ def test_legacy_install_and_no_alloc_inert(caplog):
     runner2, _ = _runner(n_layers=1)
     LB.install_smaq_hooks(runner2, mode="bogus")
     assert V.get_mode() == V.MODE_CAPTURE_ONLY
-    with caplog.at_level(logging.WARNING, logger="smaq_amd.attn"):
+    with caplog.at_level(logging.WARNING, logger="smaq.attn"):
         assert LB.enable_no_alloc(key_bits=4) is None
     assert LB._SMAQ_NO_ALLOC_CONFIG["key_bits"] == 4
     assert any("inert" in r.getMessage() for r in caplog.records)
@@ -294,3 +294,15 @@ def test_enable_no_alloc_patches_fake_vllm(monkeypatch):
     gm.shared_kv_cache_layers = {"b": "a", "c": "missing"}
     caches = {"a": 1}
     assert gm._update_hybrid_attention_mamba_layout(caches) == ["a", "b"] and caches["b"] == 1
+
+
+def test_reference_logger_names():
+    """The adapter, the backend installer and the score-kernel seam log
+    under the reference's logger names (smaq/integration/vllm.py:25,
+    smaq/vllm_attn_backend.py:14, smaq/triton_kernels.py:20), so a
+    deployment's logging configuration applies unchanged."""
+    import smaq_amd.kernels as K
+    import smaq_amd.vllm_attn_backend as B
+    assert V.logger.name == "smaq.integration.vllm"
+    assert B.logger.name == "smaq.attn"
+    assert K.logger.name == "smaq.triton"

@@ -160,6 +160,13 @@ class ColumnHistory:
             return SMAQQuantized(indices=f["k_codes"], norms=f["k_norms"], bits=qz.bits)
         return BlockVQQuantized(indices=f["k_codes"], n_blocks=qz.n_blocks, block_dim=qz.block_dim)
 
+    def allocated_bytes(self) -> int:
+        """Device bytes the column buffers hold: every field at ``capacity``
+        rows, which is up to twice the filled rows (capacity doubles when a
+        buffer is full; a grow holds the old and the new buffer until the
+        copy is done)."""
+        return sum(buf.nelement() * buf.element_size() for buf in self._bufs.values())
+
     def filled(self, lead: Optional[tuple[int, ...]] = None) -> dict[str, torch.Tensor]:
         """Rows [0, n) of every field, [lanes, n, *tail] (or [*lead, n, *tail]
         with prod(lead) == lanes; views, nothing is copied)."""

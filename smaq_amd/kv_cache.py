@@ -254,5 +254,18 @@ class SMAQKVCache:
         buf = 0 if kb is None else 2 * (kb.nelement() + vb.nelement())
         return {"quantized_keys": keys, "quantized_values": vals, "buffer": buf, "total": keys + vals + buf}
 
+    def allocated_bytes(self) -> int:
+        """Device bytes held (not in the reference): the compressed columns at
+        their capacity (up to twice the filled rows) or the quantised chunks,
+        plus the exact window's buffers (twice the window: it slides through
+        one buffer and compacts when it reaches the end)."""
+        def nb(t):
+            return 0 if t is None else t.nelement() * t.element_size()
+        hist = self._hist.allocated_bytes() if self._hist is not None else 0
+        for kq, vq in self._chunks:
+            hist += sum(nb(t) for t in (kq if isinstance(kq, tuple) else ()) if isinstance(t, torch.Tensor))
+            hist += nb(vq.data) + nb(vq.scales) + nb(vq.zeros)
+        return hist + nb(self._exact.k) + nb(self._exact.v)
+
     def get_seq_length(self) -> int:
         return self.seq_len

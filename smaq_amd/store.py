@@ -137,12 +137,30 @@ class CompressedKVStore:
         the appended chunks (smaq/store.py:116-124)."""
         return self._mem_bytes
 
+    def allocated_bytes(self) -> int:
+        """Device bytes the compressed history actually holds (not in the
+        reference): the column buffers at their capacity (up to twice
+        ``memory_bytes`` after a doubling), or the quantised chunks' tensors
+        for strategies without a column encoder."""
+        if self._hist is not None:
+            return self._hist.allocated_bytes()
+        total = 0
+        for k, v in self._chunks:
+            for t in (*_tensors_of(k), v.data, v.scales, v.zeros):
+                total += t.nelement() * t.element_size()
+        return total
+
     def reset(self):
         self._lengths.clear()
         self._hist = None
         self._chunks.clear()
         self._mem_bytes = 0
         self._flat = None
+
+
+def _tensors_of(q) -> list:
+    """The tensors of a quantised key chunk (any strategy's NamedTuple)."""
+    return [t for t in (q if isinstance(q, tuple) else ()) if isinstance(t, torch.Tensor)]
 
 
 def _value_bytes(vq: ValueQuantized) -> int:

@@ -215,3 +215,34 @@ def test_length_tensors_any_integer_dtype_or_device(dev):
     assert torch.equal(got, base), "int32 host hist_len / int32 seq_start"
     with pytest.raises(ValueError):
         kvb.attention(q, recent_k=rk, recent_v=rv, recent_len=torch.tensor([16.0, 3.0, 9.0], device=dev))
+
+
+def test_store_mixed_dtype_appends(dev):
+    """Chunks of bf16, then fp16, then fp32 keys/values appended to one store:
+    the columns widen to the promoted dtype (bf16 + fp16 -> fp32) as the
+    reference's torch.cat of its quantised chunks does (smaq/store.py:97-114),
+    so the flat cache equals the oracle's -- dtypes included, value bytes,
+    norms and value metadata bit for bit, key codes apart from at most two
+    boundary ties -- and the attention output matches."""
+    st, ref = _pair_scalar(dev, bits=3, hkv=2)
+    n = [100, 60, 50]
+    keys = sample_keys(sum(n) * 2, seed=131).reshape(sum(n), 2, 128)
+    vals = torch.randn(sum(n), 2, 128, generator=torch.Generator().manual_seed(132))
+    a = 0
+    for cnt, dt in zip(n, (torch.bfloat16, torch.float16, torch.float32)):
+        k, v = keys[a:a + cnt].to(dt), vals[a:a + cnt].to(dt)
+        st.append_chunk(k.to(dev), v.to(dev))
+        ref.append_chunk(k, v)
+        a += cnt
+    fg, fr = st.get_flat_cache(), ref.get_flat_cache()
+    assert fg.key_q.norms.dtype == fr.key_q.norms.dtype == torch.float32
+    assert fg.value_q.scales.dtype == fr.value_q.scales.dtype == torch.float32
+    # (a code byte may differ only at a boundary tie; none is expected here)
+    assert int((fg.key_q.indices.cpu() != fr.key_q.indices).sum()) <= 2
+    assert torch.equal(fg.key_q.norms.cpu(), fr.key_q.norms)
+    assert torch.equal(fg.value_q.data.cpu(), fr.value_q.data)
+    assert torch.equal(fg.value_q.scales.cpu(), fr.value_q.scales)
+    assert torch.equal(fg.value_q.zeros.cpu(), fr.value_q.zeros)
+    q = sample_keys(8, seed=133).reshape(1, 8, 128)
+    out = S.compute_hybrid_attention(q.to(dev), st, None, None, 8)
+    assert_attn_close(out, R.hybrid_attention(q, ref, None, None, 8), "mixed-dtype store")

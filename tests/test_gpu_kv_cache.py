@@ -90,3 +90,29 @@ def test_kv_cache_short_prefill_stays_exact(dev):
     torch.testing.assert_close(s, torch.matmul(q, k.transpose(-2, -1).contiguous()) / 128 ** 0.5)
     w = torch.softmax(s, dim=-1)
     torch.testing.assert_close(cache.attend(w), torch.matmul(w, k))
+
+
+def test_allocated_bytes_reports_capacity(dev):
+    """allocated_bytes (not in the reference) counts what the device holds:
+    the compressed columns at their capacity (doubling growth, so between the
+    reference's logical bytes and twice them plus the minimum allocation) and
+    the exact window's double-size buffers; memory_bytes keeps the
+    reference's logical count."""
+    calib = sample_keys(64, seed=140)
+    strat = S.SMAQFullMetricScalarStrategy(128, bits=3, device=dev).fit(calib)
+    st = S.CompressedKVStore(128, 2, key_bits=3, device=dev, key_strategy=strat)
+    keys = sample_keys(700 * 2, seed=141).reshape(700, 2, 128).bfloat16()
+    vals = torch.randn(700, 2, 128, generator=torch.Generator().manual_seed(142)).bfloat16()
+    for a, b in ((0, 300), (300, 301), (301, 700)):
+        st.append_chunk(keys[a:b].to(dev), vals[a:b].to(dev))
+    fc = st.get_flat_cache()
+    filled = sum(t.nelement() * t.element_size() for t in (fc.key_q.indices, fc.key_q.norms, fc.value_q.data,
+                                                          fc.value_q.scales, fc.value_q.zeros))
+    per_row = filled // (700 * 2)
+    alloc = st.allocated_bytes()
+    assert filled <= alloc <= 2 * filled + 256 * 2 * per_row, (filled, alloc)
+    assert st.memory_bytes() <= filled
+    cache = S.SMAQKVCache(128, buffer_size=32, device=dev, key_strategy=strat)
+    cache.prefill(keys[:200].transpose(0, 1).unsqueeze(0).to(dev), vals[:200].transpose(0, 1).unsqueeze(0).to(dev))
+    exact = 2 * (2 * 32 * 2 * 128 * 2)                      # keys + values, twice the window, bf16
+    assert cache.allocated_bytes() >= exact + cache.memory_bytes()["quantized_keys"]

@@ -230,7 +230,8 @@ typedef struct smaq_attn_params {
   long long max_hist_len;
   long long max_recent_len;
   /* 0 = run everything; else a bit mask of phases to launch, so a caller can
-     time them apart: 1 = history partials, 2 = recent partials, 4 = combine.
+     time them apart: 8 = query rotation (with rot_mt), 1 = history
+     partials, 2 = recent partials, 4 = combine.
      Phases communicate through the workspace, launched in order on one
      stream.  When the matrix-core decode kernel serves the history as one
      split per (sequence, KV head) and there is no recent part, phase 1
@@ -258,7 +259,7 @@ typedef struct smaq_attn_params {
      counters must not overlap. */
   int* arrivals;
   /* Optional query rotation (rot_mt NULL: q_hist is read as given).  With
-     rot_mt set, phase 1 first writes q_hist = (q_raw @ M^T) [* rot_scale]
+     rot_mt set, phase 8 writes q_hist = (q_raw @ M^T) [* rot_scale]
      (smaq_rotate_rows, one launch), the codec-space query that
      SMAQQuantizer.rotate_query (smaq/quantizer.py:131-136) and
      RotationAdapter.rotate_query (smaq/weighted_scalar.py:342-345) form

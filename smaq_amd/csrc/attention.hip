@@ -585,7 +585,7 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
   part.l = part.m + n_part;
   part.o = part.l + n_part;
 
-  const int phases = p.phases ? p.phases : 7;
+  const int phases = p.phases ? p.phases : 15;
   // The matrix-core decode kernel writes the output itself when the history
   // is one split and there is no recent part, or, given arrival counters,
   // merges its several splits itself (its last workgroup per sequence and KV
@@ -611,8 +611,8 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
     if (rc != SMAQ_OK) return rc;
   }
   // The query rotation (given rot_mt) is one launch into q_hist ahead of
-  // the history phase.
-  if (p.has_history && p.rot_mt && (phases & 1)) {
+  // the history phase (phase 8).
+  if (p.has_history && p.rot_mt && (phases & 8)) {
     const int rc = smaq_rotate_rows(p.q_raw, p.q_raw_dtype, (long long)p.batch * p.q_len * p.n_q_heads, p.head_dim,
                                     p.rot_mt, p.rot_scale, (float*)p.q_hist, stream);
     if (rc != SMAQ_OK) return rc;

@@ -160,15 +160,14 @@ __global__ __launch_bounds__(256) void rotate_rows128_kernel(const T* __restrict
   out[r * 128 + j] = s ? acc * s[j] : acc;
 }
 
-// More rows at head_dim 128 (a decode step of a thousand or more query
-// rows): the 2-row blocks above read the 64 KB matrix once per row pair from
-// L2, so here a block of 128 threads (one per column j) holds ROWS rows and
-// each Mt element feeds ROWS chains; the Mt loads go out CHUNK at a time.
-// Each chain is the same sequential fmaf over d, so every kernel gives the
-// same bits.  8 rows from kRot128ManyRows rows on; 4 rows (one block per CU
-// at 1024 rows, half the L2 reads of the 2-row blocks) from kRot128MidRows.
+// Many rows at head_dim 128 (a decode step of thousands of sequences): the
+// 2-row blocks above read the 64 KB matrix once per row pair from L2, so
+// here a block of 128 threads (one per column j) holds ROWS rows and each Mt
+// element feeds ROWS chains; the Mt loads go out CHUNK at a time.  Each chain
+// is the same sequential fmaf over d, so every kernel gives the same bits.
+// (At c3's 1024 rows, 4-row blocks measured no faster than the 2-row ones in
+// the whole decode step.)
 constexpr int64_t kRot128ManyRows = 4096;
-constexpr int64_t kRot128MidRows = 512;
 
 template <typename T, int ROWS, int CHUNK>
 __global__ __launch_bounds__(128) void rotate_rows128_multi_kernel(const T* __restrict__ x, int64_t rows,
@@ -363,14 +362,6 @@ extern "C" int smaq_rotate_rows(const void* x, int xdtype, long long rows, int D
   if (D == 128 && rows >= kRot128ManyRows) {
     SMAQ_DISPATCH_DTYPE(xdtype, T,
         hipLaunchKernelGGL((rotate_rows128_multi_kernel<T, 8, 32>), dim3((unsigned)((rows + 7) / 8)),
-                           dim3(128), 0, st, (const T*)x, (int64_t)rows, Mt, coord_scales, out);
-        return launch_status("smaq_rotate_rows");)
-    set_error("smaq_rotate_rows: unsupported dtype %d", xdtype);
-    return SMAQ_EUNSUPPORTED;
-  }
-  if (D == 128 && rows >= kRot128MidRows) {
-    SMAQ_DISPATCH_DTYPE(xdtype, T,
-        hipLaunchKernelGGL((rotate_rows128_multi_kernel<T, 4, 64>), dim3((unsigned)((rows + 3) / 4)),
                            dim3(128), 0, st, (const T*)x, (int64_t)rows, Mt, coord_scales, out);
         return launch_status("smaq_rotate_rows");)
     set_error("smaq_rotate_rows: unsupported dtype %d", xdtype);

@@ -217,7 +217,8 @@ class AttentionPlan:
             self.q_exact.copy_(q)
 
     def launch(self, phases: int = 0) -> torch.Tensor:
-        """Launch the attention phases (0 = all) on the current stream."""
+        """Launch the attention phases on the current stream: 0 = all, else a
+        mask of 8 (query rotation), 1 (history), 2 (recent), 4 (combine)."""
         self.params.phases = phases
         _native.attn_hybrid(self.params, self.device)
         return self.out

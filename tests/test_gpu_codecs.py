@@ -191,10 +191,9 @@ def test_scalar_dequant_scores_rotate(dev):
 def test_rotate_rows_128_chunking_and_accuracy(dev, dtype, scaled):
     """smaq_rotate_rows at head_dim 128 (the decode query rotation): one
     sequential fmaf chain per output, so 5001 rows in one call (8-row blocks,
-    the last one partial) equal the same rows in calls of 301 (2-row blocks,
-    the last one partial), 2499 and 2201 rows (4-row blocks, the last ones
-    partial) bit for bit, and match the float64 product within the rounding
-    bound of a 128-term fp32 chain."""
+    the last one partial) equal the same rows in calls of 301, 2499 and 2201
+    rows (2-row blocks, the last one partial) bit for bit, and match the
+    float64 product within the rounding bound of a 128-term fp32 chain."""
     g = torch.Generator().manual_seed(130)
     M = torch.linalg.qr(torch.randn(128, 128, generator=g, dtype=torch.float64))[0].float()
     cs = (torch.rand(128, generator=g) + 0.5) if scaled else None

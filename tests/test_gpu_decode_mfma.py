@@ -92,7 +92,7 @@ def test_mfma_decode_direct_output(dev, qdtype):
     """Contexts of at most 512 tokens give one split per (sequence, head) and
     no recent part, so the decode kernel writes the output itself (no split
     combine); a history phase followed by a separate combine phase gives the
-    same bits."""
+    same bits (the rotation, phase 8, first)."""
     strat, codec = _codec_pair(dev, 3, 320)
     hkv, g = 8, 4
     lens = [300, 512, 17, 200, 64]
@@ -110,6 +110,7 @@ def test_mfma_decode_direct_output(dev, qdtype):
     full = plan.run(q.to(dev)).clone()
     plan.out.zero_()
     plan.load_query(q.to(dev))
+    plan.launch(phases=8)      # query rotation
     plan.launch(phases=1)
     plan.launch(phases=4)
     torch.cuda.synchronize()
@@ -282,7 +283,7 @@ def test_mfma_decode_merge_with_recent(dev, odtype):
     assert torch.equal(out, again) and int(plan.arrivals.abs().sum()) == 0
     plan.out.zero_()
     plan.load_query(qd)
-    for ph in (1, 2, 4):
+    for ph in (8, 1, 2, 4):
         plan.launch(phases=ph)
     torch.cuda.synchronize()
     assert torch.equal(plan.out, out), f"merge with recent differs: {(plan.out.float() - out.float()).abs().max()}"

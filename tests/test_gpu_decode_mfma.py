@@ -330,8 +330,9 @@ def test_nan_key_norm_gives_nan_rows(dev, lens):
     softmax (smaq/score.py:61-72) returns NaN for every query row that
     scores it.  The fused paths do the same -- matrix-core decode with the
     in-kernel split merge, with the combine launch, with one split writing
-    the output directly ([400, 300]), and the generic kernels -- while every
-    other row keeps its bits."""
+    the output directly ([400, 300]), the generic kernels and the
+    matrix-core prefill -- while every other row keeps its bits (finite, for
+    the prefill)."""
     strat, _ = _codec_pair(dev, 3, 370)
     hkv, g = 2, 4
     gen = torch.Generator().manual_seed(371)
@@ -352,3 +353,8 @@ def test_nan_key_norm_gives_nan_rows(dev, lens):
             what = f"impl {impl} merge {merge}"
             assert bool(torch.isnan(out[bad]).all()), what
             assert bool(torch.equal(out[~bad], clean[impl].cpu()[~bad])), what
+    # the matrix-core prefill (16 query tokens per sequence) and its combine
+    q16 = torch.randn(len(lens), 16, hkv * g, 128, generator=gen).bfloat16().to(dev)
+    out = kvb.attention(q16, impl=3).cpu()
+    assert bool(torch.isnan(out[0, :, g:2 * g]).all()), "prefill"
+    assert not bool(torch.isnan(out[0, :, :g]).any()) and not bool(torch.isnan(out[1:]).any()), "prefill"

@@ -107,7 +107,7 @@ class AttentionPlan:
             if query_positions.numel() != B * T or query_positions.dtype.is_floating_point:
                 raise ValueError(f"query_positions must be {B * T} integer positions ([batch, q_len])")
             qp = query_positions.to(dev, torch.int64).contiguous()
-            keep.append(qp)
+            self._positions = qp
             p.q_positions = qp.data_ptr()
         p.hist_pos_offset = int(hist_pos_offset)
         p.recent_pos_offset = int(recent_pos_offset)
@@ -117,6 +117,7 @@ class AttentionPlan:
         self.hist_len = None        # the plan's own per-sequence length buffers
         self.recent_len = None      # (int64; updated in place by set_lengths)
         self._block_table = None
+        self._recent = None         # (keys, values) the plan reads; rebound by set_recent
         if has_hist:
             if fused.rot_t is not None:
                 # The library rotates the raw query itself (inside the decode
@@ -177,7 +178,7 @@ class AttentionPlan:
             rk, rv = recent_k.contiguous(), recent_v.contiguous()
             recent_len = _own_copy(_per_sequence_index(recent_len, B, dev, "recent_len"))
             self.recent_len = recent_len
-            keep += [rk, rv]
+            self._recent = (rk, rv)
             p.has_recent = 1
             p.recent_k, p.recent_v = rk.data_ptr(), rv.data_ptr()
             p.recent_dtype = _native.dtype_code(rk.dtype)
@@ -263,6 +264,32 @@ class AttentionPlan:
         bt = block_table[:B].to(self.device, torch.int32).contiguous()
         self._block_table = bt
         self.params.block_table = bt.data_ptr()
+
+    def set_recent(self, recent_k: torch.Tensor, recent_v: torch.Tensor) -> None:
+        """Point the plan at another exact recent window of the shape and
+        dtype it was built with ([B, R, Hkv, D]; copied only if not
+        contiguous)."""
+        if self._recent is None:
+            raise ValueError("plan was built without a recent window")
+        rk0 = self._recent[0]
+        for t in (recent_k, recent_v):
+            if t.shape != rk0.shape or t.dtype != rk0.dtype or t.device != rk0.device:
+                raise ValueError(f"recent window {tuple(t.shape)} {t.dtype} on {t.device} does not match the plan's "
+                                 f"{tuple(rk0.shape)} {rk0.dtype} on {rk0.device}")
+        rk, rv = recent_k.contiguous(), recent_v.contiguous()
+        self._recent = (rk, rv)
+        self.params.recent_k, self.params.recent_v = rk.data_ptr(), rv.data_ptr()
+
+    def set_query_positions(self, query_positions: torch.Tensor) -> None:
+        """New causal positions ([batch, q_len] integers) for a plan built
+        with positions."""
+        if getattr(self, "_positions", None) is None:
+            raise ValueError("plan was built without query positions")
+        if query_positions.numel() != self._positions.numel() or query_positions.dtype.is_floating_point:
+            raise ValueError(f"query_positions must be {self._positions.numel()} integer positions")
+        qp = query_positions.to(self.device, torch.int64).contiguous()
+        self._positions = qp
+        self.params.q_positions = qp.data_ptr()
 
     def run_into(self, query: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
         """``run`` writing the result straight into ``out`` (contiguous, the
@@ -359,6 +386,36 @@ def plan_hybrid_attention(
         hist_pos_offset=0, recent_pos_offset=n_all, impl=impl, **kw)
 
 
+def _store_plan(query, store, recent_k, recent_v, num_query_heads, scale, query_positions, impl):
+    """The fused plan for these inputs, kept on the store between calls: a
+    repeated call with the same query shape, the same history (token count
+    and column buffers) and a recent window of the same shape rebinds the
+    window and positions and launches, without rebuilding the plan."""
+    flat = store.get_flat_cache()
+    has_recent = recent_k is not None and recent_k.shape[0] > 0
+    hist_key = None
+    if flat is not None and flat.num_tokens >= MIN_HISTORY_FOR_SMAQ:
+        (codes, norms, vdata, vsc, vz), stride = _flat_tensors(flat)
+        hist_key = (flat.num_tokens, stride, tuple(0 if t is None else t.data_ptr() for t in
+                                                   (codes, norms, vdata, vsc, vz)))
+    key = (tuple(query.shape), query.dtype, query.device, num_query_heads, scale, impl, query_positions is None,
+           hist_key, None if not has_recent else (tuple(recent_k.shape), recent_k.dtype, recent_k.device))
+    cached = getattr(store, "_fused_plan", None)
+    if cached is not None and cached[0] == key:
+        plan = cached[1]
+        if has_recent:
+            plan.set_recent(recent_k.unsqueeze(0), recent_v.unsqueeze(0))
+        if query_positions is not None:
+            plan.set_query_positions(query_positions.reshape(1, -1))
+        return plan
+    plan = plan_hybrid_attention(query, store, recent_k, recent_v, num_query_heads, scale, query_positions, impl)
+    try:
+        store._fused_plan = (key, plan) if plan is not None else None
+    except AttributeError:
+        pass  # a store type that takes no attributes: no caching
+    return plan
+
+
 def compute_hybrid_attention(
     query: torch.Tensor,
     store: CompressedKVStore,
@@ -378,9 +435,10 @@ def compute_hybrid_attention(
     which applies no mask.  ``impl`` picks the kernels (0 automatic,
     1 generic, 2 matrix-core decode, 3 matrix-core prefill).
     """
-    plan = plan_hybrid_attention(query, store, recent_k, recent_v, num_query_heads, scale, query_positions, impl)
+    plan = _store_plan(query, store, recent_k, recent_v, num_query_heads, scale, query_positions, impl)
     if plan is not None:
-        return plan.run(query.unsqueeze(0)).squeeze(0)
+        out = torch.empty(query.shape[0], num_query_heads, store.head_dim, dtype=query.dtype, device=plan.device)
+        return plan.run_into(query.unsqueeze(0), out)
     flat = store.get_flat_cache()
     has_history = flat is not None and flat.num_tokens >= MIN_HISTORY_FOR_SMAQ
     has_recent = recent_k is not None and recent_k.shape[0] > 0

@@ -70,6 +70,7 @@ class CompressedKVStore:
         self._chunks: list[tuple[Any, ValueQuantized]] = []
         self._mem_bytes = 0
         self._flat: Optional[FlatCache] = None
+        self._fused_plan = None   # compute_hybrid_attention's kept launch (key, plan)
 
     @property
     def capabilities(self) -> CacheCapabilities:
@@ -156,6 +157,7 @@ class CompressedKVStore:
         self._chunks.clear()
         self._mem_bytes = 0
         self._flat = None
+        self._fused_plan = None   # compute_hybrid_attention's kept launch
 
 
 def _tensors_of(q) -> list:

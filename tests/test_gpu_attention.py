@@ -246,3 +246,33 @@ def test_store_mixed_dtype_appends(dev):
     q = sample_keys(8, seed=133).reshape(1, 8, 128)
     out = S.compute_hybrid_attention(q.to(dev), st, None, None, 8)
     assert_attn_close(out, R.hybrid_attention(q, ref, None, None, 8), "mixed-dtype store")
+
+
+def test_compute_hybrid_attention_keeps_its_plan(dev):
+    """Repeated compute_hybrid_attention calls over an unchanged store re-use
+    the launch kept on the store (a new recent window of the same shape is
+    rebound, not rebuilt), each call returns its own output tensor, and an
+    append replaces the plan; every result equals the oracle's."""
+    st, ref = _pair_scalar(dev, bits=3, hkv=2)
+    keys = sample_keys(400 * 2, seed=151).reshape(400, 2, 128)
+    vals = torch.randn(400, 2, 128, generator=torch.Generator().manual_seed(152))
+    st.append_chunk(keys[:300].to(dev), vals[:300].to(dev))
+    ref.append_chunk(keys[:300], vals[:300])
+    g = torch.Generator().manual_seed(153)
+    outs, plans = [], []
+    for step in range(3):
+        q = sample_keys(8, seed=160 + step).reshape(1, 8, 128)
+        kr = torch.randn(5, 2, 128, generator=g).bfloat16()
+        vr = torch.randn(5, 2, 128, generator=g).bfloat16()
+        out = S.compute_hybrid_attention(q.to(dev), st, kr.to(dev), vr.to(dev), 8)
+        assert_attn_close(out, R.hybrid_attention(q, ref, kr, vr, 8), f"kept plan step {step}")
+        outs.append(out)
+        plans.append(st._fused_plan[1])
+    assert plans[0] is plans[1] is plans[2]
+    assert outs[0].data_ptr() != outs[1].data_ptr()
+    st.append_chunk(keys[300:].to(dev), vals[300:].to(dev))
+    ref.append_chunk(keys[300:], vals[300:])
+    q = sample_keys(8, seed=170).reshape(1, 8, 128)
+    out = S.compute_hybrid_attention(q.to(dev), st, None, None, 8)
+    assert st._fused_plan[1] is not plans[0]
+    assert_attn_close(out, R.hybrid_attention(q, ref, None, None, 8), "after append")

@@ -181,7 +181,10 @@ typedef struct smaq_attn_params {
   int head_dim;     /* D */
   float scale;      /* softmax scale (1/sqrt(D) when the caller passes None) */
   /* queries, fp32 [batch][q_len][Hq][D]: q_hist is the query as the history
-     codec scores it (rotated for scalar codes), q_exact the plain query. */
+     codec scores it (rotated for scalar codes), q_exact the plain query.
+     With q_raw set (below) the recent window reads q_raw instead, and
+     q_exact is a scratch row buffer the library fills from q_raw when a
+     multi-token query takes the recent prefill path. */
   const float* q_hist;
   const float* q_exact;
   /* causal extension: NULL = no mask (reference semantics); else int64

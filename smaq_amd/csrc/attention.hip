@@ -244,7 +244,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_recent_kernel(smaq_attn_par
   for (int i = tid; i < nr * D; i += kAttnThreads) {
     const int r = i / D, d = i - r * D;
     const int row = r0 + r, t = row / g, j = row - t * g;
-    qs[r][d] = p.q_exact[(((int64_t)b * p.q_len + t) * p.n_q_heads + h * g + j) * D + d];
+    qs[r][d] = exact_query(p, (((int64_t)b * p.q_len + t) * p.n_q_heads + h * g + j) * D + d);
   }
   if (tid < nr) {
     m_s[tid] = -__builtin_inff();
@@ -362,6 +362,14 @@ __global__ __launch_bounds__(kAttnThreads) void attn_recent_kernel(smaq_attn_par
   }
 }
 
+// ----------------------------------------------------------- widen ---------
+// x (storage dtype) -> fp32, elementwise.
+template <typename T>
+__global__ __launch_bounds__(256) void widen_kernel(const T* __restrict__ x, int64_t n, float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) out[i] = Num<T>::to_f(x[i]);
+}
+
 // ------------------------------------------------------------ combine ------
 // kCombineRows query rows per workgroup (threadIdx.y), one thread per
 // output dim (threadIdx.x): fewer, larger workgroups than one per row
@@ -464,7 +472,7 @@ static Plan make_plan(const smaq_attn_params* p) {
   if (pl.mfma) split = mfma_decode_split_len(*p);
   pl.hist_split = split;
   int64_t rl = p->has_recent ? p->max_recent_len : 0;
-  pl.recent_split = 4 * kChunk;
+  pl.recent_split = (!pl.prefill && recent_decode_supported(*p)) ? recent_decode_split_len() : 4 * kChunk;
   pl.hist_lp = pl.recent_lp = 0;
   if (pl.prefill) {
     if (hl > 0) pl.hist_split = prefill_split_len(*p, hl);
@@ -559,7 +567,7 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
     SMAQ_REQUIRE(p.max_hist_len > 0, "smaq_attn_hybrid: history without tokens");
   }
   if (p.has_recent) {
-    SMAQ_REQUIRE(p.q_exact && p.recent_k && p.recent_v && p.max_recent_len > 0,
+    SMAQ_REQUIRE((p.q_exact || p.q_raw) && p.recent_k && p.recent_v && p.max_recent_len > 0,
                  "smaq_attn_hybrid: null recent pointer");
   }
   const Plan pl = make_plan(&p);
@@ -636,6 +644,20 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
       if ((rc = launch_prefill_mfma(p, pp, pl.s_hist, part, st)) != SMAQ_OK) return rc;
     }
     if (pl.s_recent > 0 && (phases & 2)) {
+      // the prefill kernel reads the plain query as fp32 rows: with a raw
+      // query handed in, the library writes them into q_exact first
+      if (p.q_raw) {
+        SMAQ_REQUIRE(p.q_exact, "smaq_attn_hybrid: the prefill recent part needs a q_exact buffer");
+        const int64_t n = (int64_t)p.batch * p.q_len * p.n_q_heads * p.head_dim;
+        const unsigned blocks = (unsigned)((n + 255) / 256);
+        switch (p.q_raw_dtype) {
+          case SMAQ_F32: hipLaunchKernelGGL(widen_kernel<float>, dim3(blocks), dim3(256), 0, st, (const float*)p.q_raw, n, (float*)p.q_exact); break;
+          case SMAQ_F16: hipLaunchKernelGGL(widen_kernel<_Float16>, dim3(blocks), dim3(256), 0, st, (const _Float16*)p.q_raw, n, (float*)p.q_exact); break;
+          default: hipLaunchKernelGGL(widen_kernel<bf16>, dim3(blocks), dim3(256), 0, st, (const bf16*)p.q_raw, n, (float*)p.q_exact); break;
+        }
+        int rc = launch_status("smaq_attn_hybrid(query widen)");
+        if (rc != SMAQ_OK) return rc;
+      }
       int rc = launch_prefill_planes_recent(p, rp, st);
       if (rc != SMAQ_OK) return rc;
       const PrefillPart pp{p.q_exact, rp.img, rp.img_lo, rp.err, p.recent_len, p.max_recent_len, rp.Lp, pl.recent_split,

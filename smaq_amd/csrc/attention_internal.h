@@ -5,6 +5,17 @@
 
 namespace smaq {
 
+// Element idx of the plain (unrotated) query as fp32: from the raw query in
+// its own dtype when the caller hands one in (p.q_raw), else from q_exact.
+__device__ __forceinline__ float exact_query(const smaq_attn_params& p, int64_t idx) {
+  if (p.q_raw == nullptr) return p.q_exact[idx];
+  switch (p.q_raw_dtype) {
+    case SMAQ_F32: return ((const float*)p.q_raw)[idx];
+    case SMAQ_F16: return Num<_Float16>::to_f(((const _Float16*)p.q_raw)[idx]);
+    default: return Num<bf16>::to_f(((const bf16*)p.q_raw)[idx]);
+  }
+}
+
 struct HistAddr {
   const long long* seq_start;  // NULL: sequence b starts at b * uniform_len
   long long uniform_len;
@@ -81,6 +92,8 @@ int launch_prefill_mfma(const smaq_attn_params& p, const PrefillPart& pp, int n_
 // generic kernel.  Writes the same partials as the generic recent kernel
 // (splits s_base .. s_base+n_splits-1).
 bool recent_decode_supported(const smaq_attn_params& p);
+// tokens per split of the decode recent window (one chunk per workgroup)
+int64_t recent_decode_split_len();
 int launch_recent_decode(const smaq_attn_params& p, const Partials& part, int s_base, int n_splits,
                          int64_t split_len, hipStream_t st);
 

@@ -8,8 +8,11 @@
 // one softmax shared with the history, the weights applied to the exact
 // values.  Here: per 64-token chunk, wave w takes tokens 16w..16w+15; a lane
 // holds a quarter of one token's key (32 dims, 16-byte loads: 4 lanes read a
-// 256-byte key row) and the same quarter of the G query rows in registers,
-// and the quarters are summed with two lane exchanges.  The online softmax
+// 256-byte key row, kept packed) and reads the same quarter of the G query
+// rows from LDS, and the quarters are summed with two lane exchanges.  At
+// <= 128 VGPRs (16-bit windows) four workgroups share a CU, so the windows
+// of a decode batch are cut into one-chunk splits that all run in one round
+// (recent_decode_split_len).  The online softmax
 // runs over the chunk (natural-log units, as the other partial writers); for
 // the weighted values lane l holds dims 2l, 2l+1 of its wave's 16 tokens (one
 // 256-byte value row per wave load).  The chunk's key and value loads are all
@@ -25,23 +28,26 @@ namespace {
 constexpr int kRD = 128;     // head_dim
 constexpr int kRChunk = 64;  // tokens per online-softmax step (16 per wave)
 
-// Eight consecutive recent-window elements (16 or 32 bytes) -> fp32.
+// 32 consecutive recent-window elements (64 or 128 bytes), kept as loaded
+// and widened on use.
 template <typename T>
-__device__ __forceinline__ void load8(const T* src, float* out) {
-  if constexpr (sizeof(T) == 2) {
-    const uint4 v = *(const uint4*)src;
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+struct Row32 {
+  static constexpr int kWords = sizeof(T) == 2 ? 16 : 32;
+  uint32_t w[kWords];
+  __device__ __forceinline__ void load(const T* src) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      out[2 * i] = Num<T>::to_f(__builtin_bit_cast(T, (uint16_t)w[i]));
-      out[2 * i + 1] = Num<T>::to_f(__builtin_bit_cast(T, (uint16_t)(w[i] >> 16)));
+    for (int i = 0; i < kWords; i += 4) {
+      const uint4 v = *(const uint4*)((const uint32_t*)src + i);
+      w[i] = v.x; w[i + 1] = v.y; w[i + 2] = v.z; w[i + 3] = v.w;
     }
-  } else {
-    const float4 a = *(const float4*)src, c = *(const float4*)(src + 4);
-    out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
-    out[4] = c.x; out[5] = c.y; out[6] = c.z; out[7] = c.w;
   }
-}
+  __device__ __forceinline__ float get(int i) const {
+    if constexpr (sizeof(T) == 2)
+      return Num<T>::to_f(__builtin_bit_cast(T, (uint16_t)(w[i >> 1] >> (16 * (i & 1)))));
+    else
+      return __builtin_bit_cast(float, w[i]);
+  }
+};
 
 // Two consecutive elements, kept as loaded (one or two dwords).
 template <typename T>
@@ -63,9 +69,15 @@ struct Pair {
   }
 };
 
+// Waves per SIMD: 4 (<= 128 VGPRs) for 16-bit windows; fp32 windows hold
+// twice the loaded words, 2.
+template <typename TR>
+constexpr int kRecentWaves = sizeof(TR) == 2 ? 4 : 2;
+
 template <typename TR, int G>
-__global__ __launch_bounds__(256) void recent_decode_kernel(smaq_attn_params p, Partials part, int s_base,
-                                                            int64_t split_len) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kRecentWaves<TR>, kRecentWaves<TR>))) void recent_decode_kernel(
+    smaq_attn_params p, Partials part, int s_base, int64_t split_len) {
+  __shared__ __attribute__((aligned(16))) float qs[G][kRD];  // the query rows
   __shared__ float sc[G][kRChunk];     // the chunk's scores, then weights
   __shared__ float m_s[G], l_s[G], a_s[G];
   __shared__ float red[4][G][kRD];     // per-wave outputs, summed at the end
@@ -80,18 +92,11 @@ __global__ __launch_bounds__(256) void recent_decode_kernel(smaq_attn_params p, 
   const TR* rv = (const TR*)p.recent_v + (int64_t)b * p.recent_batch_stride + (int64_t)h * kRD;
   const long long qpos = p.q_positions ? p.q_positions[b] : 0;
 
-  // this lane's quarter (dims 32 dq ..) of the G query rows
+  // the G query rows of this KV head, staged in LDS (lane (tq, dq) reads
+  // dims 32 dq .. of each)
   const int tq = lane & 15, dq = lane >> 4;
-  float q[G][32];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const float* qr = p.q_exact + ((int64_t)b * p.n_q_heads + h * G + g) * kRD + 32 * dq;
-#pragma unroll
-    for (int i = 0; i < 32; i += 4) {
-      const float4 v = *(const float4*)(qr + i);
-      q[g][i] = v.x; q[g][i + 1] = v.y; q[g][i + 2] = v.z; q[g][i + 3] = v.w;
-    }
-  }
+  for (int i = tid; i < G * kRD; i += 256)
+    qs[i / kRD][i % kRD] = exact_query(p, ((int64_t)b * p.n_q_heads + h * G) * kRD + i);
   if (tid < G) {
     m_s[tid] = -__builtin_inff();
     l_s[tid] = 0.0f;
@@ -106,22 +111,29 @@ __global__ __launch_bounds__(256) void recent_decode_kernel(smaq_attn_params p, 
     // loads: this lane's key quarter (token 16w + tq) and its wave's 16 value
     // pairs; rows past the window read its last token and are dropped
     const int kt = 16 * w + tq;
-    float k[32];
-    {
-      const TR* kr = rk + (c0 + min(kt, nt - 1)) * tstride + 32 * dq;
-#pragma unroll
-      for (int i = 0; i < 32; i += 8) load8(kr + i, k + i);
-    }
+    Row32<TR> k;
+    k.load(rk + (c0 + min(kt, nt - 1)) * tstride + 32 * dq);
     Pair<TR> v[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) v[i].load(rv + (c0 + min(16 * w + i, nt - 1)) * tstride + 2 * lane);
     // scores: quarter dot products, summed over the 4 lanes of a token
     float acc[G];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      acc[g] = 0.0f;
+    for (int g = 0; g < G; ++g) acc[g] = 0.0f;
 #pragma unroll
-      for (int i = 0; i < 32; ++i) acc[g] = fmaf(q[g][i], k[i], acc[g]);
+    for (int i = 0; i < 32; i += 4) {
+      const float k0 = k.get(i), k1 = k.get(i + 1), k2 = k.get(i + 2), k3 = k.get(i + 3);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float4 qv = *(const float4*)&qs[g][32 * dq + i];
+        acc[g] = fmaf(qv.x, k0, acc[g]);
+        acc[g] = fmaf(qv.y, k1, acc[g]);
+        acc[g] = fmaf(qv.z, k2, acc[g]);
+        acc[g] = fmaf(qv.w, k3, acc[g]);
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
       acc[g] += __shfl_xor(acc[g], 16, 64);
       acc[g] += __shfl_xor(acc[g], 32, 64);
     }
@@ -200,13 +212,15 @@ void launch_g(const smaq_attn_params& p, const Partials& part, int s_base, int n
 
 }  // namespace
 
+int64_t recent_decode_split_len() { return kRChunk; }
+
 bool recent_decode_supported(const smaq_attn_params& p) {
   const int g = p.n_q_heads / p.n_kv_heads;
   return p.impl != 1 && p.has_recent && p.q_len == 1 && p.head_dim == kRD && (g == 1 || g == 2 || g == 4) &&
          (p.recent_dtype == SMAQ_F32 || p.recent_dtype == SMAQ_F16 || p.recent_dtype == SMAQ_BF16) &&
          // 16-byte key loads and 4- or 8-byte value loads at element offsets
          // that are multiples of 8 and 2
-         (((uintptr_t)p.recent_k | (uintptr_t)p.recent_v) & 15) == 0 && ((uintptr_t)p.q_exact & 15) == 0;
+         (((uintptr_t)p.recent_k | (uintptr_t)p.recent_v) & 15) == 0;
 }
 
 int launch_recent_decode(const smaq_attn_params& p, const Partials& part, int s_base, int n_splits,

@@ -185,7 +185,6 @@ class AttentionPlan:
             p.recent_len = None if recent_len is None else recent_len.data_ptr()
             p.recent_batch_stride = rk.shape[1] * rk.shape[2] * rk.shape[3]
             p.max_recent_len = int(max_recent_len)
-        self.needs_exact = has_recent
         self.out = torch.empty(B, T, Hq, D, dtype=out_dtype, device=dev)
         p.out = self.out.data_ptr()
         p.out_dtype = _native.dtype_code(out_dtype)
@@ -199,9 +198,9 @@ class AttentionPlan:
     def load_query(self, query: torch.Tensor) -> None:
         """Hand a query to the plan.  With a rotated codec the library reads
         the query as given (fp32/fp16/bf16, contiguous, 16-byte aligned;
-        anything else is copied to fp32 first) and rotates it during the
-        launch; the fp32 copy is made only when the exact (recent-window) path
-        or an unrotated codec reads it."""
+        anything else is copied to fp32 first): it rotates it for the history
+        and the recent window reads it directly, so no copy is made.  An
+        unrotated codec scores the fp32 copy."""
         q = query.reshape(self.shape)
         if self.rot_t is not None:
             if q.device != self.device:
@@ -212,8 +211,6 @@ class AttentionPlan:
             self._q_raw = q  # kept alive until the next load
             self.params.q_raw = q.data_ptr()
             self.params.q_raw_dtype = _native.dtype_code(q.dtype)
-            if self.needs_exact:
-                self.q_exact.copy_(q)
         else:
             self.q_exact.copy_(q)
 

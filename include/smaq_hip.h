@@ -59,6 +59,30 @@ int smaq_dequant_values(const void* data, const void* scales, const void* zeros,
                         long long rows, int D, int bits, int group, float* out, void* stream);
 
 /*
+ * Weighted sum over packed values.  Replaces the compressed term of
+ * SMAQKVCache.attend (smaq/kv_cache.py:247-252), torch.matmul(w,
+ * dequantize_values(vq)): out[b][q][d] = sum_n w[b][q][n] * v[b][n][d] with
+ * v = float(code) * scale + zero (smaq/kv_cache.py:94-103), summed in fp32
+ * without writing v out.  Deterministic: fixed token splits summed in order.
+ *   w fp32, element (b, q, n) at w[b * w_bstride + q * w_qstride + n];
+ *   data: row n of batch b at data + b * d_bstride + n * (D / vpb) bytes
+ *   (vpb = 4, 2, 1 codes per byte for 2-, 4-, other-bit codes);
+ *   scales, zeros: row n of batch b at b * s_bstride + n * (D / group)
+ *   elements, in sdtype; out [batch][nq][D] fp32, overwritten.
+ *   workspace: smaq_apply_values_workspace_bytes(batch, nq, N, D) bytes
+ *   (0: none needed).
+ * Layouts: a value row must be a power-of-two number (<= 64) of 4-byte words,
+ * each inside one group (D = 128: 2-bit with group % 16 == 0, 4-bit with
+ * group % 8 == 0, 8-bit with group % 4 == 0); others return
+ * SMAQ_EUNSUPPORTED.
+ */
+long long smaq_apply_values_workspace_bytes(long long batch, long long nq, long long N, int D);
+int smaq_apply_values(const float* w, long long w_bstride, long long w_qstride, long long batch, long long nq,
+                      long long N, int D, const void* data, long long d_bstride, int bits, int group,
+                      const void* scales, const void* zeros, long long s_bstride, int sdtype, float* out,
+                      void* workspace, long long workspace_bytes, void* stream);
+
+/*
  * Scalar key encoder.  Replaces SMAQQuantizer.quantize (smaq/quantizer.py:138-145)
  * and RotationAdapter.quantize (smaq/weighted_scalar.py:347-355):
  * n = ||k|| (key dtype), u = k / (n + 1e-10) (key dtype), y = u @ M^T (fp32),

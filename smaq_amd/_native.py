@@ -84,6 +84,9 @@ _SIGS = {
     "smaq_attn_hybrid": (c_int, [ctypes.POINTER(AttnParams), c_void_p]),
     "smaq_attn_hybrid_noalloc": (c_int, [ctypes.POINTER(AttnParams), c_void_p]),
     "smaq_probe_read": (c_int, [c_void_p, c_ll, c_void_p, c_void_p]),
+    "smaq_apply_values_workspace_bytes": (c_ll, [c_ll, c_ll, c_ll, c_int]),
+    "smaq_apply_values": (c_int, [c_void_p, c_ll, c_ll, c_ll, c_ll, c_ll, c_int, c_void_p, c_ll, c_int, c_int,
+                                  c_void_p, c_void_p, c_ll, c_int, c_void_p, c_void_p, c_ll, c_void_p]),
 }
 
 # Size of the built-in workspace of smaq_attn_hybrid_noalloc
@@ -269,6 +272,60 @@ def dequant_values(data, scales, zeros, bits: int, group_size: int) -> torch.Ten
     _check(lib().smaq_dequant_values(_ptr(data), _ptr(scales), _ptr(zeros), dtype_code(scales.dtype),
                                      rows, D, bits, group_size, _ptr(out), _stream(dev)),
            "smaq_dequant_values")
+    return out
+
+
+def apply_values_supported(D: int, bits: int, group_size: int) -> bool:
+    """Whether smaq_apply_values takes this value layout: a row of D codes is
+    a power-of-two number (<= 64) of 4-byte words, each inside one group."""
+    vpb = 4 if bits == 2 else (2 if bits == 4 else 1)
+    dpl = 4 * vpb
+    if not (1 <= bits <= 8 and 0 < D <= 512 and group_size > 0 and D % group_size == 0 and D % dpl == 0):
+        return False
+    lanes = D // dpl
+    return lanes <= 64 and lanes & (lanes - 1) == 0 and group_size % dpl == 0
+
+
+def apply_values(w: torch.Tensor, data: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor, bits: int,
+                 group_size: int) -> torch.Tensor:
+    """w [*lead, nq, N] fp32 applied to packed values data [*lead, N, D/vpb]
+    (scales, zeros [*lead, N, D/group]) -> [*lead, nq, D] fp32, the value
+    rows decoded on the fly.  Row-dense views with the lead dims a fixed stride
+    apart (column buffers) are read in place."""
+    dev = require_gpu(w, data, scales, zeros)
+    if w.dtype != torch.float32:
+        raise ValueError(f"apply_values: weights must be float32, got {w.dtype}")
+    if scales.dtype != zeros.dtype or scales.shape != zeros.shape:
+        raise ValueError("apply_values: scales and zeros differ in dtype or shape")
+    lead, (nq, N) = tuple(w.shape[:-2]), tuple(w.shape[-2:])
+    if tuple(data.shape[:-2]) != lead or data.shape[-2] != N or tuple(scales.shape[:-1]) != tuple(data.shape[:-1]):
+        raise ValueError(f"apply_values: weights {tuple(w.shape)} do not match values {tuple(data.shape)}")
+    vpb = 4 if bits == 2 else (2 if bits == 4 else 1)
+    rb, ng = data.shape[-1], scales.shape[-1]
+    D = rb * vpb
+    if ng * group_size != D:
+        raise ValueError(f"apply_values: {ng} groups of {group_size} do not cover head_dim {D}")
+    batch = 1
+    for x in lead:
+        batch *= int(x)
+    out = torch.empty(*lead, nq, D, dtype=torch.float32, device=dev)
+    if batch == 0 or nq == 0:
+        return out
+    w3 = w.reshape(batch, nq, N)
+    if N > 1 and w3.stride(2) != 1:
+        w3 = w3.contiguous()
+    d3 = data.reshape(batch, N, rb)
+    if d3.stride(2) != 1 or (N > 1 and d3.stride(1) != rb):
+        d3 = d3.contiguous()
+    s3, z3 = scales.reshape(batch, N, ng), zeros.reshape(batch, N, ng)
+    if (s3.stride() != z3.stride() or s3.stride(2) != 1 or (N > 1 and s3.stride(1) != ng)):
+        s3, z3 = s3.contiguous(), z3.contiguous()
+    ws_bytes = lib().smaq_apply_values_workspace_bytes(batch, nq, N, D)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
+    _check(lib().smaq_apply_values(_ptr(w3), w3.stride(0), w3.stride(1), batch, nq, N, D, _ptr(d3), d3.stride(0),
+                                   bits, group_size, _ptr(s3), _ptr(z3), s3.stride(0), dtype_code(s3.dtype),
+                                   _ptr(out), _ptr(ws), max(ws_bytes, 0), _stream(dev)),
+           "smaq_apply_values")
     return out
 
 

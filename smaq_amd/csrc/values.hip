@@ -7,6 +7,7 @@
 //   scale = max(scale, rnd(1e-10))  -- clamp bound converted to the dtype
 //   min / max propagate NaN (torch's reductions)
 //   code  = clamp(rint(rnd(rnd(v - min) / scale)), 0, levels), NaN -> 0
+#include <algorithm>
 #include <type_traits>
 
 #include "smaq_common.h"
@@ -204,6 +205,104 @@ static int launch_dequant(const void* data, const void* scales, const void* zero
   return launch_status("smaq_dequant_values");
 }
 
+
+// ------------------------------------------------- weighted packed values --
+// out[b][q][d] = sum_n w[b][q][n] * (code[b][n][d] * scale + zero): the
+// compressed term of SMAQKVCache.attend, the dequantised values never
+// written out.  A lane holds one 4-byte word of a value row (4 * VPB
+// codes, all of one group); L = D / (4 VPB) lanes cover a row and a wave
+// load covers 64 / L rows.  Workgroup (split s, batch b) sums its token range
+// per lane, across the lanes of a column by exchanges and across its four
+// waves through LDS, in a fixed order; the splits are summed in split order
+// by a second launch.
+constexpr int kAvThreads = 256;
+constexpr int kAvQ = 4;         // query rows per pass over the tokens
+constexpr int kAvMaxD = 512;
+
+template <int VPB, typename T>
+__global__ __launch_bounds__(kAvThreads) void apply_values_kernel(
+    const float* __restrict__ w, int64_t w_bstride, int64_t w_qstride, int nq, int64_t N, int D,
+    const uint8_t* __restrict__ data, int64_t d_bstride, const T* __restrict__ scales,
+    const T* __restrict__ zeros, int64_t s_bstride, int group, int64_t split_len, float* __restrict__ part,
+    int64_t part_split) {
+  constexpr int DPL = 4 * VPB;  // codes per lane
+  constexpr int BITS = VPB == 4 ? 2 : (VPB == 2 ? 4 : 8);
+  constexpr uint32_t MASK = (1u << BITS) - 1u;
+  __shared__ float red[4][kAvQ][kAvMaxD];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int s = blockIdx.x, b = blockIdx.y;
+  const int L = D / DPL, tpw = 64 / L;
+  const int dl = lane & (L - 1), tl = lane / L;
+  const int d0 = dl * DPL;
+  const int row_bytes = D / VPB, ng = D / group;
+  const int64_t t0 = (int64_t)s * split_len;
+  const int64_t t1 = min(N, t0 + split_len);
+  const uint8_t* dcol = data + (int64_t)b * d_bstride + 4 * dl;
+  const T* scol = scales + (int64_t)b * s_bstride + d0 / group;
+  const T* zcol = zeros + (int64_t)b * s_bstride + d0 / group;
+  const float* wb = w + (int64_t)b * w_bstride;
+  float* pout = part + (int64_t)s * part_split + (int64_t)b * nq * D;
+  for (int q0 = 0; q0 < nq; q0 += kAvQ) {
+    const int nqq = min(kAvQ, nq - q0);
+    float acc[kAvQ][DPL];
+#pragma unroll
+    for (int q = 0; q < kAvQ; ++q)
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) acc[q][e] = 0.0f;
+#pragma unroll 2
+    for (int64_t t = t0 + (int64_t)wv * tpw + tl; t < t1; t += 4 * tpw) {
+      const uint32_t word = *(const uint32_t*)(dcol + t * row_bytes);
+      const float sc = Num<T>::to_f(scol[t * ng]);
+      const float z = Num<T>::to_f(zcol[t * ng]);
+      float v[DPL];
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) v[e] = (float)((word >> (BITS * e)) & MASK) * sc + z;  // fp-contract off
+#pragma unroll
+      for (int q = 0; q < kAvQ; ++q) {
+        if (q < nqq) {
+          const float wq = wb[(int64_t)(q0 + q) * w_qstride + t];
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) acc[q][e] = __builtin_fmaf(wq, v[e], acc[q][e]);
+        }
+      }
+    }
+    // the rows of a wave load share no column: sum the lanes of a column
+    for (int off = L; off < 64; off <<= 1)
+#pragma unroll
+      for (int q = 0; q < kAvQ; ++q)
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) acc[q][e] += __shfl_xor(acc[q][e], off, 64);
+    if (tl == 0)
+#pragma unroll
+      for (int q = 0; q < kAvQ; ++q)
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) red[wv][q][d0 + e] = acc[q][e];
+    __syncthreads();
+    for (int i = tid; i < nqq * D; i += kAvThreads) {
+      const int q = i / D, d = i - q * D;
+      pout[(int64_t)(q0 + q) * D + d] = (red[0][q][d] + red[1][q][d]) + (red[2][q][d] + red[3][q][d]);
+    }
+    __syncthreads();
+  }
+}
+
+// out[i] = sum over splits, in split order
+__global__ __launch_bounds__(256) void apply_values_reduce_kernel(const float* __restrict__ part, int n_splits,
+                                                                  int64_t total, float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  float acc = part[i];
+  for (int k = 1; k < n_splits; ++k) acc += part[(int64_t)k * total + i];
+  out[i] = acc;
+}
+
+// token splits of a launch: at least 512 tokens each, about 2048 workgroups
+static int64_t apply_values_splits(long long batch, long long N) {
+  const int64_t by_len = std::max<int64_t>(1, (N + 511) / 512);
+  const int64_t by_grid = std::max<int64_t>(1, (2048 + batch - 1) / std::max<long long>(1, batch));
+  return std::min<int64_t>(std::min(by_len, by_grid), 65535);
+}
+
 }  // namespace smaq
 
 using namespace smaq;
@@ -253,4 +352,69 @@ extern "C" int smaq_dequant_values(const void* data, const void* scales, const v
   }
   set_error("smaq_dequant_values: unsupported dtype %d", sdtype);
   return SMAQ_EUNSUPPORTED;
+}
+
+extern "C" long long smaq_apply_values_workspace_bytes(long long batch, long long nq, long long N, int D) {
+  if (batch <= 0 || nq <= 0 || D <= 0) return 0;
+  const int64_t n_splits = apply_values_splits(batch, N);
+  return n_splits > 1 ? (long long)(n_splits * batch * nq * D * (int64_t)sizeof(float)) : 0;
+}
+
+extern "C" int smaq_apply_values(const float* w, long long w_bstride, long long w_qstride, long long batch,
+                                 long long nq, long long N, int D, const void* data, long long d_bstride, int bits,
+                                 int group, const void* scales, const void* zeros, long long s_bstride, int sdtype,
+                                 float* out, void* workspace, long long workspace_bytes, void* stream) {
+  SMAQ_REQUIRE(batch >= 0 && nq >= 0 && N >= 0, "smaq_apply_values: negative shape");
+  if (batch == 0 || nq == 0) return SMAQ_OK;
+  SMAQ_REQUIRE(out && (N == 0 || (w && data && scales && zeros)), "smaq_apply_values: null pointer");
+  SMAQ_REQUIRE(batch <= 65535, "smaq_apply_values: batch %lld above 65535", batch);
+  SMAQ_REQUIRE(bits >= 1 && bits <= 8, "smaq_apply_values: bits must be in [1, 8], got %d", bits);
+  SMAQ_REQUIRE(D > 0 && D <= kAvMaxD && group > 0 && D % group == 0,
+               "smaq_apply_values: head_dim %d (at most %d) must be divisible by group_size %d", D, kAvMaxD, group);
+  const int vpb = value_codes_per_byte(bits), dpl = 4 * vpb;
+  const int lanes = D / dpl;
+  if (!(D % dpl == 0 && lanes <= 64 && (lanes & (lanes - 1)) == 0 && group % dpl == 0)) {
+    set_error("smaq_apply_values: unsupported layout (head_dim %d, %d-bit codes, group %d): a value row must be "
+              "a power-of-two number (<= 64) of 4-byte words each inside one group",
+              D, bits, group);
+    return SMAQ_EUNSUPPORTED;
+  }
+  SMAQ_REQUIRE(((uintptr_t)data % 4) == 0 && d_bstride % 4 == 0, "smaq_apply_values: value rows must be 4-byte aligned");
+  const int64_t n_splits = apply_values_splits(batch, N);
+  const int64_t split_len = std::max<int64_t>(1, (N + n_splits - 1) / n_splits);
+  const int64_t total = batch * nq * (int64_t)D;
+  float* part = out;
+  if (n_splits > 1) {
+    SMAQ_REQUIRE(workspace && workspace_bytes >= n_splits * total * (int64_t)sizeof(float),
+                 "smaq_apply_values: workspace of %lld bytes below %lld", workspace_bytes,
+                 (long long)(n_splits * total * (int64_t)sizeof(float)));
+    part = (float*)workspace;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)n_splits, (unsigned)batch);
+#define SMAQ_AV(VPB, T)                                                                                           \
+  hipLaunchKernelGGL((apply_values_kernel<VPB, T>), grid, dim3(kAvThreads), 0, st, w, (int64_t)w_bstride,          \
+                     (int64_t)w_qstride, (int)nq, (int64_t)N, D, (const uint8_t*)data, (int64_t)d_bstride,           \
+                     (const T*)scales, (const T*)zeros, (int64_t)s_bstride, group, split_len, part, total)
+#define SMAQ_AV_T(VPB)                                      \
+  switch (sdtype) {                                         \
+    case SMAQ_F32: SMAQ_AV(VPB, float); break;              \
+    case SMAQ_F16: SMAQ_AV(VPB, _Float16); break;           \
+    case SMAQ_BF16: SMAQ_AV(VPB, bf16); break;              \
+    default: set_error("smaq_apply_values: unsupported dtype %d", sdtype); return SMAQ_EUNSUPPORTED; \
+  }
+  if (vpb == 4) {
+    SMAQ_AV_T(4)
+  } else if (vpb == 2) {
+    SMAQ_AV_T(2)
+  } else {
+    SMAQ_AV_T(1)
+  }
+#undef SMAQ_AV_T
+#undef SMAQ_AV
+  int rc = launch_status("smaq_apply_values");
+  if (rc != SMAQ_OK || n_splits == 1) return rc;
+  hipLaunchKernelGGL(apply_values_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, part,
+                     (int)n_splits, total, out);
+  return launch_status("smaq_apply_values(reduce)");
 }

@@ -21,6 +21,7 @@ from typing import Any, Optional
 
 import torch
 
+from smaq_amd import _native
 from smaq_amd.calibration import IdentityCalibrationProvider
 from smaq_amd.columns import ColumnHistory, codec_kind
 from smaq_amd.core import CacheCapabilities, CalibrationProvider
@@ -234,7 +235,15 @@ class SMAQKVCache:
         vq = self.value_quantized
         if vq is not None:
             nq = vq.data.shape[-2]
-            out = torch.matmul(attn_weights[..., col:col + nq], dequantize_values(vq, self.value_group_size))
+            w = attn_weights[..., col:col + nq]
+            bits = vq.bits if len(vq) > 3 else 2
+            if (w.is_cuda and w.dtype == torch.float32 and w.shape[:-2] == vq.data.shape[:-2]
+                    and _native.apply_values_supported(self.head_dim, bits, self.value_group_size)):
+                # the packed codes decoded inside the weighted sum: no fp32
+                # value rows (512 B per token-head at D = 128) are written
+                out = _native.apply_values(w, vq.data, vq.scales, vq.zeros, bits, self.value_group_size)
+            else:
+                out = torch.matmul(w, dequantize_values(vq, self.value_group_size))
             col += nq
         vb = self.value_buffer
         if vb is not None:

@@ -116,3 +116,30 @@ def test_allocated_bytes_reports_capacity(dev):
     cache.prefill(keys[:200].transpose(0, 1).unsqueeze(0).to(dev), vals[:200].transpose(0, 1).unsqueeze(0).to(dev))
     exact = 2 * (2 * 32 * 2 * 128 * 2)                      # keys + values, twice the window, bf16
     assert cache.allocated_bytes() >= exact + cache.memory_bytes()["quantized_keys"]
+
+
+@pytest.mark.parametrize("bits,group", [(2, 32), (4, 32), (8, 32), (2, 16)])
+@pytest.mark.parametrize("sdtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("N", [0, 1, 37, 3000])
+def test_apply_values_matches_dequantized_matmul(dev, bits, group, sdtype, N):
+    """smaq_apply_values (the compressed term of SMAQKVCache.attend,
+    smaq/kv_cache.py:247-252) against the oracle's fp32 dequantised values
+    (smaq/kv_cache.py:94-103) times the weights in float64: within 2e-3 abs +
+    1e-3 rel, and within 1e-5 of the float64 sum (fp32 accumulation); 6 query
+    rows (more than one 4-row pass), several token splits at N = 3000, and a
+    weight view sliced out of a wider matrix as attend passes it."""
+    from smaq_amd import _native
+    B, H, nq = 2, 3, 6
+    g = torch.Generator().manual_seed(150 + bits + N)
+    vals = (torch.randn(B, H, N, 128, generator=g) * 3.0).to(sdtype)
+    ref_v = R.quantize_values(vals, bits=bits, group_size=group)
+    w_all = torch.softmax(torch.randn(B, H, nq, N + 9, generator=g) * 2.0, dim=-1)
+    w = w_all[..., 4:4 + N]
+    v_hat = R.dequantize_values(ref_v, group)
+    ref = torch.matmul(w.double(), v_hat.double())
+    got = _native.apply_values(w_all.to(dev)[..., 4:4 + N], ref_v.data.to(dev), ref_v.scales.to(dev),
+                               ref_v.zeros.to(dev), bits, group).cpu()
+    assert got.shape == (B, H, nq, 128) and got.dtype == torch.float32
+    err = (got.double() - ref).abs()
+    assert bool((err <= 2e-3 + 1e-3 * ref.abs()).all()), float(err.max())
+    assert float(err.max()) <= 1e-5 * max(1.0, float(ref.abs().max())), float(err.max())

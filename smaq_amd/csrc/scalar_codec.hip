@@ -127,77 +127,66 @@ __global__ __launch_bounds__(kEncThreads) void encode_scalar_kernel(
 }
 
 // out[r][j] = (sum_d x[r][d] * Mt[d][j]) [* s[j]], one sequential fmaf chain
-// over d per output (the reference's CPU matmul order).  A block holds
+// over d per output.  A block holds
 // kRotRows rows in LDS and one thread per column j; each Mt element loaded
 // feeds kRotRows independent chains.
 constexpr int kRotRows = 8;
 
-// The same product for head_dim 128 with one thread per output element, so
-// that a decode step's few thousand query rows fill the GPU: a block holds 2
-// rows (staged in LDS, read as broadcasts) and each thread runs its column's
-// fmaf chain with the Mt loads issued 32 ahead.
-template <typename T>
+// The same product for head_dim 128 (the decode query rotation), shaped for
+// latency: a step's few thousand rows are one short launch ahead of the
+// decode kernel.  A block of 256 threads holds ROWS rows in LDS; thread
+// (dq = t / 32, cg = t % 32) loads the 16 x 4 elements Mt[16 dq .. 16 dq + 15]
+// [4 cg .. 4 cg + 3] at once (one memory round trip), runs a 16-term fmaf chain
+// per row and column, and the eight partial chains of an output are summed
+// in a fixed tree, ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7)).  Every
+// output's rounding is thus fixed by the row alone (not by the blocking),
+// and its error bound is that of a 19-term chain rather than 128.
+template <typename T, int ROWS>
 __global__ __launch_bounds__(256) void rotate_rows128_kernel(const T* __restrict__ x, int64_t rows,
                                                              const float* __restrict__ Mt,
                                                              const float* __restrict__ s,
                                                              float* __restrict__ out) {
-  __shared__ float xs[2][128];
-  const int t = threadIdx.x;
-  const int rr = t >> 7, j = t & 127;
-  const int64_t r = (int64_t)blockIdx.x * 2 + rr;
-  xs[rr][j] = r < rows ? Num<T>::to_f(x[r * 128 + j]) : 0.0f;
-  __syncthreads();
-  if (r >= rows) return;
-  float acc = 0.0f;
-#pragma unroll
-  for (int d0 = 0; d0 < 128; d0 += 32) {
-    float m[32];
-#pragma unroll
-    for (int i = 0; i < 32; ++i) m[i] = Mt[(d0 + i) * 128 + j];
-#pragma unroll
-    for (int i = 0; i < 32; ++i) acc = fmaf(xs[rr][d0 + i], m[i], acc);
-  }
-  out[r * 128 + j] = s ? acc * s[j] : acc;
-}
-
-// Many rows at head_dim 128 (a decode step of thousands of sequences): the
-// 2-row blocks above read the 64 KB matrix once per row pair from L2, so
-// here a block of 128 threads (one per column j) holds ROWS rows and each Mt
-// element feeds ROWS chains; the Mt loads go out CHUNK at a time.  Each chain
-// is the same sequential fmaf over d, so every kernel gives the same bits.
-// (At c3's 1024 rows, 4-row blocks measured no faster than the 2-row ones in
-// the whole decode step.)
-constexpr int64_t kRot128ManyRows = 4096;
-
-template <typename T, int ROWS, int CHUNK>
-__global__ __launch_bounds__(128) void rotate_rows128_multi_kernel(const T* __restrict__ x, int64_t rows,
-                                                                   const float* __restrict__ Mt,
-                                                                   const float* __restrict__ s,
-                                                                   float* __restrict__ out) {
   __shared__ float xs[ROWS][128];
-  const int j = threadIdx.x;
+  __shared__ float part[ROWS][8][128];
+  const int t = threadIdx.x;
+  const int cg = t & 31, dq = t >> 5;
   const int64_t r0 = (int64_t)blockIdx.x * ROWS;
+  float4 m[16];
 #pragma unroll
-  for (int i = 0; i < ROWS; ++i) xs[i][j] = r0 + i < rows ? Num<T>::to_f(x[(r0 + i) * 128 + j]) : 0.0f;
-  __syncthreads();
-  float acc[ROWS];
+  for (int i = 0; i < 16; ++i) m[i] = *(const float4*)(Mt + (16 * dq + i) * 128 + 4 * cg);
 #pragma unroll
-  for (int i = 0; i < ROWS; ++i) acc[i] = 0.0f;
-#pragma unroll
-  for (int d0 = 0; d0 < 128; d0 += CHUNK) {
-    float m[CHUNK];
-#pragma unroll
-    for (int i = 0; i < CHUNK; ++i) m[i] = Mt[(d0 + i) * 128 + j];
-#pragma unroll
-    for (int i = 0; i < CHUNK; ++i)
-#pragma unroll
-      for (int r = 0; r < ROWS; ++r) acc[r] = fmaf(xs[r][d0 + i], m[i], acc[r]);
+  for (int e = t; e < ROWS * 128; e += 256) {
+    const int64_t r = r0 + e / 128;
+    xs[e / 128][e % 128] = r < rows ? Num<T>::to_f(x[r * 128 + e % 128]) : 0.0f;
   }
-  const float sj = s ? s[j] : 1.0f;
+  __syncthreads();
+#pragma unroll 2
+  for (int r = 0; r < ROWS; ++r) {
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
 #pragma unroll
-  for (int r = 0; r < ROWS; ++r)
-    if (r0 + r < rows) out[(r0 + r) * 128 + j] = s ? acc[r] * sj : acc[r];
+    for (int i = 0; i < 16; ++i) {
+      const float xv = xs[r][16 * dq + i];
+      a0 = fmaf(xv, m[i].x, a0);
+      a1 = fmaf(xv, m[i].y, a1);
+      a2 = fmaf(xv, m[i].z, a2);
+      a3 = fmaf(xv, m[i].w, a3);
+    }
+    *(float4*)&part[r][dq][4 * cg] = make_float4(a0, a1, a2, a3);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int e = t; e < ROWS * 128; e += 256) {
+    const int r = e / 128, j = e % 128;
+    if (r0 + r >= rows) continue;
+    const float v = ((part[r][0][j] + part[r][1][j]) + (part[r][2][j] + part[r][3][j])) +
+                    ((part[r][4][j] + part[r][5][j]) + (part[r][6][j] + part[r][7][j]));
+    out[(r0 + r) * 128 + j] = s ? v * s[j] : v;
+  }
 }
+
+// rows per block: 4 up to 2048 rows (a c3 step's 1024 rows: 256 blocks), 16
+// beyond (fewer copies of the 64 KB matrix read from L2)
+constexpr int64_t kRot128ManyRows = 2048;
 
 template <typename T>
 __global__ __launch_bounds__(1024) void rotate_rows_kernel(const T* __restrict__ x, int64_t rows,
@@ -359,19 +348,15 @@ extern "C" int smaq_rotate_rows(const void* x, int xdtype, long long rows, int D
   const int64_t blocks = ((int64_t)rows + kRotRows - 1) / kRotRows;
   SMAQ_REQUIRE(blocks < (1ll << 31), "smaq_rotate_rows: too many rows");
   hipStream_t st = (hipStream_t)stream;
-  if (D == 128 && rows >= kRot128ManyRows) {
+  if (D == 128 && ((uintptr_t)Mt & 15) == 0) {  // (16-byte loads of Mt)
+    const int rpb = rows > kRot128ManyRows ? 16 : 4;
+    SMAQ_REQUIRE((rows + rpb - 1) / rpb < (1ll << 31), "smaq_rotate_rows: too many rows");
+    const dim3 grid((unsigned)((rows + rpb - 1) / rpb));
     SMAQ_DISPATCH_DTYPE(xdtype, T,
-        hipLaunchKernelGGL((rotate_rows128_multi_kernel<T, 8, 32>), dim3((unsigned)((rows + 7) / 8)),
-                           dim3(128), 0, st, (const T*)x, (int64_t)rows, Mt, coord_scales, out);
-        return launch_status("smaq_rotate_rows");)
-    set_error("smaq_rotate_rows: unsupported dtype %d", xdtype);
-    return SMAQ_EUNSUPPORTED;
-  }
-  if (D == 128) {
-    SMAQ_REQUIRE((rows + 1) / 2 < (1ll << 31), "smaq_rotate_rows: too many rows");
-    SMAQ_DISPATCH_DTYPE(xdtype, T,
-        hipLaunchKernelGGL(rotate_rows128_kernel<T>, dim3((unsigned)((rows + 1) / 2)), dim3(256), 0, st,
-                           (const T*)x, (int64_t)rows, Mt, coord_scales, out);
+        if (rpb == 16) hipLaunchKernelGGL((rotate_rows128_kernel<T, 16>), grid, dim3(256), 0, st, (const T*)x,
+                                          (int64_t)rows, Mt, coord_scales, out);
+        else hipLaunchKernelGGL((rotate_rows128_kernel<T, 4>), grid, dim3(256), 0, st, (const T*)x, (int64_t)rows,
+                                Mt, coord_scales, out);
         return launch_status("smaq_rotate_rows");)
     set_error("smaq_rotate_rows: unsupported dtype %d", xdtype);
     return SMAQ_EUNSUPPORTED;

@@ -16,7 +16,9 @@
 // runs over the chunk (natural-log units, as the other partial writers); for
 // the weighted values lane l holds dims 2l, 2l+1 of its wave's 16 tokens (one
 // 256-byte value row per wave load).  The chunk's key and value loads are all
-// issued before any is used, so a chunk costs one memory round trip.
+// issued before any is used, and the first chunk's together with the
+// window length and the query rows, so a one-chunk split costs one memory
+// round trip.
 #include <math.h>
 
 #include "attention_internal.h"
@@ -84,17 +86,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kRecentWave
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int64_t len = p.recent_len ? min((int64_t)p.recent_len[b], (int64_t)p.max_recent_len) : p.max_recent_len;
   const int64_t t0 = (int64_t)s * split_len;
-  const int64_t t1 = min(len, t0 + split_len);
   const int64_t tstride = (int64_t)p.n_kv_heads * kRD;
   const TR* rk = (const TR*)p.recent_k + (int64_t)b * p.recent_batch_stride + (int64_t)h * kRD;
   const TR* rv = (const TR*)p.recent_v + (int64_t)b * p.recent_batch_stride + (int64_t)h * kRD;
+  const int tq = lane & 15, dq = lane >> 4;
+  const int kt = 16 * w + tq;
+  // A chunk's loads: this lane's key quarter (token 16w + tq) and its wave's
+  // 16 value pairs.  Rows are clamped to the buffer's last row
+  // (max_recent_len - 1), not to the sequence's length, so the first chunk's
+  // loads go out before the length, the query and the barrier; rows past
+  // the window are dropped below.
+  const int64_t last_row = p.max_recent_len - 1;
+  Row32<TR> k;
+  Pair<TR> v[16];
+  auto load_chunk = [&](int64_t c0) {
+    k.load(rk + min(c0 + kt, last_row) * tstride + 32 * dq);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i].load(rv + min(c0 + 16 * w + i, last_row) * tstride + 2 * lane);
+  };
+  load_chunk(t0);
+  const int64_t len = p.recent_len ? min((int64_t)p.recent_len[b], (int64_t)p.max_recent_len) : p.max_recent_len;
+  const int64_t t1 = min(len, t0 + split_len);
   const long long qpos = p.q_positions ? p.q_positions[b] : 0;
 
   // the G query rows of this KV head, staged in LDS (lane (tq, dq) reads
   // dims 32 dq .. of each)
-  const int tq = lane & 15, dq = lane >> 4;
   for (int i = tid; i < G * kRD; i += 256)
     qs[i / kRD][i % kRD] = exact_query(p, ((int64_t)b * p.n_q_heads + h * G) * kRD + i);
   if (tid < G) {
@@ -108,14 +125,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kRecentWave
 
   for (int64_t c0 = t0; c0 < t1; c0 += kRChunk) {
     const int nt = (int)min((int64_t)kRChunk, t1 - c0);
-    // loads: this lane's key quarter (token 16w + tq) and its wave's 16 value
-    // pairs; rows past the window read its last token and are dropped
-    const int kt = 16 * w + tq;
-    Row32<TR> k;
-    k.load(rk + (c0 + min(kt, nt - 1)) * tstride + 32 * dq);
-    Pair<TR> v[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) v[i].load(rv + (c0 + min(16 * w + i, nt - 1)) * tstride + 2 * lane);
+    if (c0 > t0) load_chunk(c0);
     // scores: quarter dot products, summed over the 4 lanes of a token
     float acc[G];
 #pragma unroll

@@ -614,13 +614,19 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
     return launch_status("smaq_attn_hybrid(recent)");
   };
   const bool recent_first = merge && pl.s_recent > 0;
-  if (recent_first) {
+  // The query rotation (given rot_mt) is one launch into q_hist ahead of
+  // the history phase (phase 8); when the recent window goes first as well
+  // (and has the decode kernel), one launch runs both side by side.
+  const bool rotation = p.has_history && p.rot_mt && (phases & 8);
+  const bool paired = recent_first && rotation && !pl.prefill && rotate_recent_supported(p);
+  if (paired) {
+    const int rc = launch_rotate_recent(p, part, pl.s_hist, pl.s_recent, pl.recent_split, st);
+    if (rc != SMAQ_OK) return rc;
+  } else if (recent_first) {
     const int rc = launch_recent();
     if (rc != SMAQ_OK) return rc;
   }
-  // The query rotation (given rot_mt) is one launch into q_hist ahead of
-  // the history phase (phase 8).
-  if (p.has_history && p.rot_mt && (phases & 8)) {
+  if (rotation && !paired) {
     const int rc = smaq_rotate_rows(p.q_raw, p.q_raw_dtype, (long long)p.batch * p.q_len * p.n_q_heads, p.head_dim,
                                     p.rot_mt, p.rot_scale, (float*)p.q_hist, stream);
     if (rc != SMAQ_OK) return rc;

@@ -96,6 +96,12 @@ bool recent_decode_supported(const smaq_attn_params& p);
 int64_t recent_decode_split_len();
 int launch_recent_decode(const smaq_attn_params& p, const Partials& part, int s_base, int n_splits,
                          int64_t split_len, hipStream_t st);
+// The query rotation (phase 8, into q_hist) and the decode recent window
+// (phase 2) in one launch; supported when both are (head_dim 128, a 16-byte
+// aligned rot_mt, a raw query).
+bool rotate_recent_supported(const smaq_attn_params& p);
+int launch_rotate_recent(const smaq_attn_params& p, const Partials& part, int s_base, int n_splits,
+                         int64_t split_len, hipStream_t st);
 
 // MFMA decode path (attention_mfma.hip).  Returns true when it can serve
 // these parameters (history only, decode shape, supported formats).

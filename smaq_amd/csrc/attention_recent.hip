@@ -22,6 +22,7 @@
 #include <math.h>
 
 #include "attention_internal.h"
+#include "rotate128.h"
 
 namespace smaq {
 
@@ -76,16 +77,25 @@ struct Pair {
 template <typename TR>
 constexpr int kRecentWaves = sizeof(TR) == 2 ? 4 : 2;
 
-template <typename TR, int G>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kRecentWaves<TR>, kRecentWaves<TR>))) void recent_decode_kernel(
-    smaq_attn_params p, Partials part, int s_base, int64_t split_len) {
-  __shared__ __attribute__((aligned(16))) float qs[G][kRD];  // the query rows
-  __shared__ float sc[G][kRChunk];     // the chunk's scores, then weights
-  __shared__ float m_s[G], l_s[G], a_s[G];
-  __shared__ float red[4][G][kRD];     // per-wave outputs, summed at the end
+template <int G>
+struct RecentLds {
+  __attribute__((aligned(16))) float qs[G][kRD];  // the query rows
+  float sc[G][kRChunk];                            // the chunk's scores, then weights
+  float m_s[G], l_s[G], a_s[G];
+  float red[4][G][kRD];                            // per-wave outputs, summed at the end
+};
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+// Split s of the window of (KV head h, sequence b); tid = thread index.
+template <typename TR, int G>
+__device__ __forceinline__ void recent_block(RecentLds<G>& L, const smaq_attn_params& p, const Partials& part,
+                                             int s_base, int64_t split_len, int s, int h, int b, int tid) {
+  auto& qs = L.qs;
+  auto& sc = L.sc;
+  auto& m_s = L.m_s;
+  auto& l_s = L.l_s;
+  auto& a_s = L.a_s;
+  auto& red = L.red;
+  const int lane = tid & 63, w = tid >> 6;
   const int64_t t0 = (int64_t)s * split_len;
   const int64_t tstride = (int64_t)p.n_kv_heads * kRD;
   const TR* rk = (const TR*)p.recent_k + (int64_t)b * p.recent_batch_stride + (int64_t)h * kRD;
@@ -209,6 +219,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kRecentWave
   }
 }
 
+template <typename TR, int G>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kRecentWaves<TR>, kRecentWaves<TR>))) void recent_decode_kernel(
+    smaq_attn_params p, Partials part, int s_base, int64_t split_len) {
+  __shared__ RecentLds<G> lds;
+  recent_block<TR, G>(lds, p, part, s_base, split_len, blockIdx.x, blockIdx.y, blockIdx.z, threadIdx.x);
+}
+
+// The query rotation (into q_hist) and the recent window in one launch: they
+// are independent (the window reads the raw query), so the shorter one runs
+// beside the longer instead of after it.  Blocks [0, n_rot) rotate 4 rows
+// each (rotate128.h); block n_rot + ((b * Hkv + h) * n_splits + s) takes split
+// s of (KV head h, sequence b).
+template <typename TR, int G>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kRecentWaves<TR>, kRecentWaves<TR>))) void rotate_recent_kernel(
+    smaq_attn_params p, Partials part, int s_base, int n_splits, int64_t split_len, int n_rot) {
+  __shared__ union {
+    RecentLds<G> r;
+    Rot128Lds<4> q;
+  } lds;
+  const int bx = blockIdx.x, tid = threadIdx.x;
+  if (bx < n_rot) {
+    rotate128_block<4>(lds.q, p.q_raw, p.q_raw_dtype, (int64_t)p.batch * p.q_len * p.n_q_heads, p.rot_mt,
+                       p.rot_scale, (float*)p.q_hist, bx, tid);
+    return;
+  }
+  const int r = bx - n_rot;
+  const int s = r % n_splits, hb = r / n_splits;
+  recent_block<TR, G>(lds.r, p, part, s_base, split_len, s, hb % p.n_kv_heads, hb / p.n_kv_heads, tid);
+}
+
 template <typename TR>
 void launch_g(const smaq_attn_params& p, const Partials& part, int s_base, int n_splits, int64_t split_len,
               hipStream_t st) {
@@ -231,6 +271,36 @@ bool recent_decode_supported(const smaq_attn_params& p) {
          // 16-byte key loads and 4- or 8-byte value loads at element offsets
          // that are multiples of 8 and 2
          (((uintptr_t)p.recent_k | (uintptr_t)p.recent_v) & 15) == 0;
+}
+
+template <typename TR>
+void launch_rg(const smaq_attn_params& p, const Partials& part, int s_base, int n_splits, int64_t split_len,
+               hipStream_t st) {
+  const int64_t rows = (int64_t)p.batch * p.q_len * p.n_q_heads;
+  const int n_rot = (int)((rows + 3) / 4);
+  const dim3 grid((unsigned)(n_rot + (int64_t)n_splits * p.n_kv_heads * p.batch));
+  switch (p.n_q_heads / p.n_kv_heads) {
+    case 1: hipLaunchKernelGGL((rotate_recent_kernel<TR, 1>), grid, dim3(256), 0, st, p, part, s_base, n_splits, split_len, n_rot); break;
+    case 2: hipLaunchKernelGGL((rotate_recent_kernel<TR, 2>), grid, dim3(256), 0, st, p, part, s_base, n_splits, split_len, n_rot); break;
+    default: hipLaunchKernelGGL((rotate_recent_kernel<TR, 4>), grid, dim3(256), 0, st, p, part, s_base, n_splits, split_len, n_rot); break;
+  }
+}
+
+bool rotate_recent_supported(const smaq_attn_params& p) {
+  const int64_t rows = (int64_t)p.batch * p.q_len * p.n_q_heads;
+  return recent_decode_supported(p) && p.rot_mt && p.q_raw && p.q_hist && ((uintptr_t)p.rot_mt & 15) == 0 &&
+         (p.q_raw_dtype == SMAQ_F32 || p.q_raw_dtype == SMAQ_F16 || p.q_raw_dtype == SMAQ_BF16) &&
+         (rows + 3) / 4 + (int64_t)p.n_kv_heads * p.batch * 64 < (1ll << 31);
+}
+
+int launch_rotate_recent(const smaq_attn_params& p, const Partials& part, int s_base, int n_splits,
+                         int64_t split_len, hipStream_t st) {
+  switch (p.recent_dtype) {
+    case SMAQ_F32: launch_rg<float>(p, part, s_base, n_splits, split_len, st); break;
+    case SMAQ_F16: launch_rg<_Float16>(p, part, s_base, n_splits, split_len, st); break;
+    default: launch_rg<bf16>(p, part, s_base, n_splits, split_len, st); break;
+  }
+  return launch_status("smaq_attn_hybrid(rotation + recent)");
 }
 
 int launch_recent_decode(const smaq_attn_params& p, const Partials& part, int s_base, int n_splits,

@@ -16,6 +16,7 @@
 #include <type_traits>
 
 #include "encode_internal.h"
+#include "rotate128.h"
 
 namespace smaq {
 
@@ -132,61 +133,16 @@ __global__ __launch_bounds__(kEncThreads) void encode_scalar_kernel(
 // feeds kRotRows independent chains.
 constexpr int kRotRows = 8;
 
-// The same product for head_dim 128 (the decode query rotation), shaped for
-// latency: a step's few thousand rows are one short launch ahead of the
-// decode kernel.  A block of 256 threads holds ROWS rows in LDS; thread
-// (dq = t / 32, cg = t % 32) loads the 16 x 4 elements Mt[16 dq .. 16 dq + 15]
-// [4 cg .. 4 cg + 3] at once (one memory round trip), runs a 16-term fmaf chain
-// per row and column, and the eight partial chains of an output are summed
-// in a fixed tree, ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7)).  Every
-// output's rounding is thus fixed by the row alone (not by the blocking),
-// and its error bound is that of a 19-term chain rather than 128.
-template <typename T, int ROWS>
-__global__ __launch_bounds__(256) void rotate_rows128_kernel(const T* __restrict__ x, int64_t rows,
+// The same product for head_dim 128: rotate128_block (rotate128.h), one
+// memory round trip for the matrix and a fixed summation tree per output.
+template <int ROWS>
+__global__ __launch_bounds__(256) void rotate_rows128_kernel(const void* __restrict__ x, int xdtype, int64_t rows,
                                                              const float* __restrict__ Mt,
                                                              const float* __restrict__ s,
                                                              float* __restrict__ out) {
-  __shared__ float xs[ROWS][128];
-  __shared__ float part[ROWS][8][128];
-  const int t = threadIdx.x;
-  const int cg = t & 31, dq = t >> 5;
-  const int64_t r0 = (int64_t)blockIdx.x * ROWS;
-  float4 m[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) m[i] = *(const float4*)(Mt + (16 * dq + i) * 128 + 4 * cg);
-#pragma unroll
-  for (int e = t; e < ROWS * 128; e += 256) {
-    const int64_t r = r0 + e / 128;
-    xs[e / 128][e % 128] = r < rows ? Num<T>::to_f(x[r * 128 + e % 128]) : 0.0f;
-  }
-  __syncthreads();
-#pragma unroll 2
-  for (int r = 0; r < ROWS; ++r) {
-    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float xv = xs[r][16 * dq + i];
-      a0 = fmaf(xv, m[i].x, a0);
-      a1 = fmaf(xv, m[i].y, a1);
-      a2 = fmaf(xv, m[i].z, a2);
-      a3 = fmaf(xv, m[i].w, a3);
-    }
-    *(float4*)&part[r][dq][4 * cg] = make_float4(a0, a1, a2, a3);
-  }
-  __syncthreads();
-#pragma unroll
-  for (int e = t; e < ROWS * 128; e += 256) {
-    const int r = e / 128, j = e % 128;
-    if (r0 + r >= rows) continue;
-    const float v = ((part[r][0][j] + part[r][1][j]) + (part[r][2][j] + part[r][3][j])) +
-                    ((part[r][4][j] + part[r][5][j]) + (part[r][6][j] + part[r][7][j]));
-    out[(r0 + r) * 128 + j] = s ? v * s[j] : v;
-  }
+  __shared__ Rot128Lds<ROWS> lds;
+  rotate128_block<ROWS>(lds, x, xdtype, rows, Mt, s, out, blockIdx.x, threadIdx.x);
 }
-
-// rows per block: 4 up to 2048 rows (a c3 step's 1024 rows: 256 blocks), 16
-// beyond (fewer copies of the 64 KB matrix read from L2)
-constexpr int64_t kRot128ManyRows = 2048;
 
 template <typename T>
 __global__ __launch_bounds__(1024) void rotate_rows_kernel(const T* __restrict__ x, int64_t rows,
@@ -352,14 +308,17 @@ extern "C" int smaq_rotate_rows(const void* x, int xdtype, long long rows, int D
     const int rpb = rows > kRot128ManyRows ? 16 : 4;
     SMAQ_REQUIRE((rows + rpb - 1) / rpb < (1ll << 31), "smaq_rotate_rows: too many rows");
     const dim3 grid((unsigned)((rows + rpb - 1) / rpb));
-    SMAQ_DISPATCH_DTYPE(xdtype, T,
-        if (rpb == 16) hipLaunchKernelGGL((rotate_rows128_kernel<T, 16>), grid, dim3(256), 0, st, (const T*)x,
-                                          (int64_t)rows, Mt, coord_scales, out);
-        else hipLaunchKernelGGL((rotate_rows128_kernel<T, 4>), grid, dim3(256), 0, st, (const T*)x, (int64_t)rows,
-                                Mt, coord_scales, out);
-        return launch_status("smaq_rotate_rows");)
-    set_error("smaq_rotate_rows: unsupported dtype %d", xdtype);
-    return SMAQ_EUNSUPPORTED;
+    if (xdtype != SMAQ_F32 && xdtype != SMAQ_F16 && xdtype != SMAQ_BF16) {
+      set_error("smaq_rotate_rows: unsupported dtype %d", xdtype);
+      return SMAQ_EUNSUPPORTED;
+    }
+    if (rpb == 16)
+      hipLaunchKernelGGL(rotate_rows128_kernel<16>, grid, dim3(256), 0, st, x, xdtype, (int64_t)rows, Mt,
+                         coord_scales, out);
+    else
+      hipLaunchKernelGGL(rotate_rows128_kernel<4>, grid, dim3(256), 0, st, x, xdtype, (int64_t)rows, Mt,
+                         coord_scales, out);
+    return launch_status("smaq_rotate_rows");
   }
   SMAQ_DISPATCH_DTYPE(xdtype, T,
       hipLaunchKernelGGL(rotate_rows_kernel<T>, dim3((unsigned)blocks), dim3(D),

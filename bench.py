@@ -54,7 +54,8 @@ F16_PEAK_TFLOPS = 2500.0
 # hi/lo split weight against exact 2-bit codes, fp32 softmax and accumulation.
 DECODE_DTYPE = "bf16 storage; QK 3x f16 hi/lo MFMA (~22-bit), PV 2x bf16 hi/lo MFMA on exact codes, fp32 accumulate"
 PREFILL_DTYPE = ("fp16 storage; QK f16 hi/lo keys x f16 queries (2x f16 MFMA, +1 when a query is not f16-exact), "
-                 "PV f16 values x f16 weights (1x f16 MFMA; hi/lo weights for fp32 outputs), fp32 accumulate")
+                 "PV f16 values x f16 hi/lo weights (2x f16 MFMA; +1 with a value-lo plane on key ranges whose "
+                 "f16 value rounding exceeds 1.96e-3), fp32 accumulate")
 ENCODE_DTYPE = "bf16 in; fp32-exact distances (f16 hi/lo MFMA + exact recount), u8 indices, 2-bit values"
 
 

@@ -450,8 +450,25 @@ struct Plan {
   // matrix-core decode with one workgroup per (sequence, KV head) and
   // per-sequence lengths: dispatch the longest sequences first
   bool longest_first;
+  // ... as work items (n_items > 0): the sequences past the first round of
+  // workgroup slots run in up to s_hist pieces of about piece_len tokens
+  int n_items, first_round;
+  int64_t piece_len;
   int64_t hist_lp, recent_lp;  // prefill plane lengths
 };
+
+// Longest-first pieces (matrix-core decode, ragged lengths, more sequences
+// than one round of workgroup slots holds): the sequences that start after
+// the first round run in pieces of about kDecodePiece tokens (at most
+// kDecodeMaxPieces, so longer histories take longer pieces), merged by the
+// kernel's arrival counters.  In one split per sequence, the long units
+// dispatched into the slots that free up last form the end of the launch,
+// when most slots are already idle.
+#ifndef SMAQ_DECODE_PIECE
+#define SMAQ_DECODE_PIECE 4096
+#endif
+constexpr int64_t kDecodePiece = SMAQ_DECODE_PIECE;
+constexpr int kDecodeMaxPieces = 8;
 
 static int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
 
@@ -489,7 +506,31 @@ static Plan make_plan(const smaq_attn_params* p) {
   // first).  More splits instead cost more than they balance: each
   // workgroup's start is a chain of dependent memory round trips.
   pl.longest_first = pl.mfma && p->hist_len != nullptr && pl.s_hist == 1 && p->batch > 1;
+  pl.n_items = pl.first_round = 0;
+  pl.piece_len = 0;
+  const int phases = p->phases ? p->phases : 15;
+  if (pl.longest_first && kDecodePiece > 0 && p->arrivals && (pl.s_recent == 0 || (phases & 3) == 3)) {
+    const bool wide = p->norm_dtype == SMAQ_F32 || p->val_dtype == SMAQ_F32;
+    const int first_round = device_cu_count() * (wide ? 3 : 4) / p->n_kv_heads;
+    constexpr int64_t step = kMfmaDecodeStep;
+    int64_t piece = (hl + kDecodeMaxPieces - 1) / kDecodeMaxPieces;
+    piece = piece < kDecodePiece ? kDecodePiece : piece;
+    piece = (piece + step - 1) / step * step;
+    const int max_pieces = (int)((hl + piece - 1) / piece);
+    if (p->batch > first_round && max_pieces >= 2) {
+      pl.first_round = first_round;
+      pl.piece_len = piece;
+      pl.s_hist = max_pieces;
+      pl.n_items = first_round + (p->batch - first_round) * max_pieces;
+    }
+  }
   return pl;
+}
+
+// Bytes of the longest-first order (int per sequence) or its work items
+// (16 bytes each).
+static int64_t order_bytes(const smaq_attn_params* p, const Plan& pl) {
+  return pl.n_items > 0 ? (int64_t)pl.n_items * 16 : (int64_t)p->batch * (int64_t)sizeof(int);
 }
 
 // Bytes of the partials (m, l, o) and the offset of the longest-first order.
@@ -508,7 +549,7 @@ extern "C" long long smaq_attn_workspace_bytes(const smaq_attn_params* p) {
   if (!p || p->n_kv_heads <= 0 || p->n_q_heads % p->n_kv_heads) return -1;
   const Plan pl = make_plan(p);
   int64_t bytes = partial_bytes(p, pl);
-  if (pl.longest_first) bytes = align256(bytes) + (int64_t)p->batch * (int64_t)sizeof(int);
+  if (pl.longest_first) bytes = align256(bytes) + order_bytes(p, pl);
   if (pl.prefill) {
     // tile images, value-lo planes and tile errors of each part
     bytes = align256(bytes) + prefill_planes_bytes(p->batch, p->n_kv_heads, pl.hist_lp) +
@@ -598,10 +639,12 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
   // is one split and there is no recent part, or, given arrival counters,
   // merges its several splits itself (its last workgroup per sequence and KV
   // head): no combine launch.
-  const bool direct = pl.mfma && pl.s_hist == 1 && pl.s_recent == 0;
+  // (In item mode: the sequences of one piece.)
+  const bool direct = pl.mfma && pl.s_recent == 0 && (pl.s_hist == 1 || pl.n_items > 0);
   // With a recent part the decode kernel merges the recent window's partials
   // too; the recent phase then runs first, in the same call.
-  const bool merge = pl.mfma && !direct && p.arrivals != nullptr && (pl.s_recent == 0 || (phases & 3) == 3);
+  const bool merge = pl.mfma && (!direct || pl.n_items > 0) && p.arrivals != nullptr &&
+                     (pl.s_recent == 0 || (phases & 3) == 3);
   auto launch_recent = [&]() -> int {
     if (recent_decode_supported(p)) return launch_recent_decode(p, part, pl.s_hist, pl.s_recent, pl.recent_split, st);
     dim3 grid(pl.s_recent, p.n_kv_heads * pl.row_tiles, p.batch);
@@ -678,9 +721,12 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
       int* order = nullptr;
       if (pl.longest_first) {
         order = (int*)((char*)p.workspace + align256(partial_bytes(&p, pl)));
-        if ((rc = launch_decode_order(p, order, st)) != SMAQ_OK) return rc;
+        rc = pl.n_items > 0
+                 ? launch_decode_items(p, pl.first_round, pl.s_hist, pl.piece_len, pl.n_items, order, st)
+                 : launch_decode_order(p, order, st);
+        if (rc != SMAQ_OK) return rc;
       }
-      rc = launch_mfma_decode(p, a, part, pl.s_hist, direct, merge, order, st);
+      rc = launch_mfma_decode(p, a, part, pl.s_hist, direct, merge, order, pl.n_items, st);
       if (rc != SMAQ_OK) return rc;
     } else if (p.key_format == SMAQ_KEY_SCALAR) {
       switch (p.norm_dtype) {

@@ -106,16 +106,26 @@ int launch_rotate_recent(const smaq_attn_params& p, const Partials& part, int s_
 // MFMA decode path (attention_mfma.hip).  Returns true when it can serve
 // these parameters (history only, decode shape, supported formats).
 bool mfma_decode_supported(const smaq_attn_params& p);
+// Tokens per step of a decode workgroup (4 waves x 32-token tiles): split and
+// piece boundaries are multiples of it.
+constexpr int kMfmaDecodeStep = 128;
 int64_t mfma_decode_split_len(const smaq_attn_params& p);
 // `order` (NULL: sequence b runs as grid row b) lists the sequences in the
 // order their workgroups are dispatched; launch_decode_order fills it with
 // the sequences by history length, longest first.
 int launch_decode_order(const smaq_attn_params& p, int* order, hipStream_t st);
+// The longest-first order as `n_items` work items (16 bytes each, at
+// `items`): the sequences ranked first_round and later run in up to
+// max_pieces pieces of about piece_len tokens.
+int launch_decode_items(const smaq_attn_params& p, int first_round, int max_pieces, int64_t piece_len,
+                        int n_items, void* items, hipStream_t st);
 // With `direct` (one split and no recent part) the kernel writes the final
 // output itself, and no split combine is needed; with `merge` (several
 // splits, no recent part, p.arrivals set) the last workgroup of each
-// (sequence, KV head) merges the splits and writes the output.
+// (sequence, KV head) merges the splits and writes the output.  items > 0:
+// `order` holds that many work items (launch_decode_items), n_splits is
+// the most pieces of a sequence, and `merge` is required.
 int launch_mfma_decode(const smaq_attn_params& p, const HistAddr& a, const Partials& part,
-                       int n_splits, bool direct, bool merge, const int* order, hipStream_t st);
+                       int n_splits, bool direct, bool merge, const int* order, int items, hipStream_t st);
 
 }  // namespace smaq

@@ -47,6 +47,7 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kMWaves = 4;
 constexpr int kMTile = 32;
+static_assert(kMWaves * kMTile == kMfmaDecodeStep, "decode step");
 constexpr int kVRow = 80;   // bytes per code-byte row of the spread value tile (64 + 16 pad)
 constexpr int kARow = 144;  // bytes per row of the staged PV A operand (64 hi + 64 lo + 16 pad)
 // The softmax reference maximum is raised only when a score exceeds it by
@@ -73,10 +74,22 @@ struct SplitRule {
   int n_cu;   // workgroups per round-slot (the device's CU count)
   int slots;  // round-slots per CU (at most kMaxSlots)
   int tilt;   // weight step per slot; tilt * (slots - 1) < kSplitWeight
-  int direct; // one split and no recent part: write the final output
+  int direct; // no recent part: a (sequence, KV head) of one split writes
+              // the final output
   int merge;  // arrival counters given (several splits, or a recent part
               // whose partials an earlier launch wrote): the last workgroup
               // of each (sequence, KV head) merges and writes the output
+  int pieces; // grid rows are work items (DecodeItem), not sequences: the
+              // sequences past the first round of workgroup slots run in up
+              // to n_splits pieces each
+  int items;  // grid rows in item mode
+};
+
+// A work item of the longest-first piece schedule: tokens [t0, t1) of
+// sequence seq, piece `piece` of `count`.  seq < 0: no work (the grid is
+// sized for the most items the lengths could need).
+struct DecodeItem {
+  int seq, t0, t1, meta;  // meta = count << 16 | piece
 };
 constexpr int kSplitWeight = 64;
 
@@ -361,7 +374,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
   // this lane's two softmax tokens: C-layout values 2*bank, 2*bank + 1
   const int tokA = bank < 2 ? 4 * kg + 2 * bank : 16 + 4 * kg + 2 * (bank - 2);
   const int tq = lane & 7, pq = lane >> 3;           // value loader: tokens 4tq.., bytes 4pq..
-  const int s = gz;
   // per-sequence lookups go through the scalar cache (no vector-memory wait
   // in the prologue)
   typedef const __attribute__((address_space(4))) int* ConstIntPtr;
@@ -373,18 +385,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
   // dispatch order) takes 8 * Hkv consecutive workgroups f = base + 8 h + i,
   // which puts every head of sequence i on one XCD and its shared lines in
   // one L2 (c5: HBM traffic +6.0% -> +0.8% over the algorithmic bytes).
+  // In item mode the same grouping runs over work items (the pieces of a
+  // sequence are consecutive items).
   int hsel = gx, osel = gy;
   if (order) {
     const int hk = p.n_kv_heads;
     const int f = gx + hk * gy;
-    if (f < (p.batch / 8) * 8 * hk) {
+    const int rows = rule.pieces ? rule.items : p.batch;
+    if (f < (rows / 8) * 8 * hk) {
       const int grp = f / (8 * hk), rem = f - grp * 8 * hk;
       hsel = rem >> 3;
       osel = 8 * grp + (rem & 7);
     }
   }
   const int h = __builtin_amdgcn_readfirstlane(hsel);
-  const int b = order ? ((ConstIntPtr)order)[__builtin_amdgcn_readfirstlane(osel)] : gy;
+  int b, s, nsplit;
+  int64_t s0 = 0, s1 = 0;
+  if (rule.pieces) {
+    const ConstIntPtr it = (ConstIntPtr)order + 4 * __builtin_amdgcn_readfirstlane(osel);
+    const int seq = it[0], t0 = it[1], t1 = it[2], meta = it[3];  // one 16-byte scalar load
+    b = __builtin_amdgcn_readfirstlane(seq);
+    if (b < 0) return;  // no work (uniform over the workgroup)
+    s0 = __builtin_amdgcn_readfirstlane(t0);
+    s1 = __builtin_amdgcn_readfirstlane(t1);
+    s = __builtin_amdgcn_readfirstlane(meta & 0xffff);
+    nsplit = __builtin_amdgcn_readfirstlane(meta >> 16);
+  } else {
+    b = order ? ((ConstIntPtr)order)[__builtin_amdgcn_readfirstlane(osel)] : gy;
+    s = gz;
+    nsplit = rule.n_splits;
+  }
   const int Q = p.n_q_heads / p.n_kv_heads;  // query rows (decode: one token)
   constexpr uint32_t kMask = (1u << KBITS) - 1u;
   constexpr float kLog2e = 1.4426950408889634f;
@@ -416,11 +446,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
 
   // ---- split range: split s of this sequence and head holds
   // tokens [s0, s1) (wave-uniform values are pinned to SGPRs so the tile
-  // loop's control flow and address arithmetic stay scalar)
-  const int64_t len =
-      uniform64(p.hist_len ? min(((ConstI64Ptr)p.hist_len)[b], (int64_t)p.max_hist_len) : p.max_hist_len);
-  int64_t s0 = 0, s1 = len;
-  if (rule.n_splits > 1) {
+  // loop's control flow and address arithmetic stay scalar); an item
+  // carries its range
+  if (!rule.pieces) {
+    s1 = uniform64(p.hist_len ? min(((ConstI64Ptr)p.hist_len)[b], (int64_t)p.max_hist_len) : p.max_hist_len);
+  }
+  if (!rule.pieces && rule.n_splits > 1) {
+    const int64_t len = s1;
     // (a shared boundary is computed by the same expression for both of its
     // splits, so rounding cannot open a gap or an overlap)
     const int units = p.n_kv_heads * p.batch, u = h + p.n_kv_heads * gy;
@@ -550,13 +582,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
   // MI355X, the rotation alone takes the load stream from 5.6 to 5.9 TB/s.
   // The next row is formed without a branch: with a branch at the loop top
   // the compiler waits for every load of the tile there instead of for each
-  // array when it is first used.
+  // array when it is first used.  The start follows from the (KV head,
+  // sequence, split) only, not from the grid position, which a longest-first
+  // order assigns by atomics within a length bucket: the summation order, so
+  // the output bits, must not depend on the schedule.
   const int64_t n_steps = (s1 - s0) / (kMWaves * kMTile);
   constexpr int64_t kStep = kMWaves * kMTile;
   const bool rot = !paged && even_rows && n_steps > 0;
   const int K = __builtin_amdgcn_readfirstlane((int)(rot ? n_steps : 1));
   const int r = __builtin_amdgcn_readfirstlane(
-      (int)(((unsigned)gx * 7u + (unsigned)gy * 13u + (unsigned)gz * 5u) % (unsigned)K));
+      (int)(((unsigned)h * 7u + (unsigned)b * 13u + (unsigned)s * 5u) % (unsigned)K));
   const int64_t base = uniform64(contig_base + s0 + (int64_t)wu * kMTile);  // step 0 of this wave
   const int64_t wrap = (int64_t)K * kStep;
   const int64_t rot_end = base + wrap;
@@ -944,6 +979,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
     red_l[w][lane] = l_run;
   }
   __syncthreads();
+  // a (sequence, KV head) of one split and no recent part: the final output
+  const bool direct = rule.direct && nsplit == 1;
   // ---- merge the 4 waves into this split's partial (natural-log units).
   // Each thread takes two adjacent dims of one query row and reads all its
   // LDS operands before using any (waves without tokens, l = 0, are skipped).
@@ -975,7 +1012,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
     // a NaN score makes the reference's softmax row NaN: the partial's sum
     // carries it to the merge (which would otherwise drop the partial)
     if (poisoned) L = kQuietNaN;
-    if (rule.direct) {
+    if (direct) {
       // the output itself: the split combine's arithmetic for one partial
       // (o * (1 / l), zero without tokens), in the output dtype
       const float inv = L > 0.0f ? 1.0f / L : 0.0f;
@@ -1001,7 +1038,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
       }
     }
   }
-  if (!rule.merge) return;
+  if (direct || !rule.merge) return;
   // ---- split merge.  Once every thread has seen its agent-coherent partial
   // stores complete (vmcnt 0), one thread counts the workgroup in with a
   // vector atomic; the workgroup that completes the count is the unit's
@@ -1017,7 +1054,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
   if (tid == 0) {
     int* const cnt = p.arrivals + ((int64_t)b * p.n_kv_heads + h);
     const int before = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int last = before == rule.n_splits - 1 ? 1 : 0;
+    const int last = before == nsplit - 1 ? 1 : 0;
     if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     last_split = last;
   }
@@ -1040,7 +1077,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
         lv[k] = 0.0f;
         mv[k] = -__builtin_inff();
         ov[k] = f32x2{0.0f, 0.0f};
-        if (c0 + k < S) {
+        // history partials [0, nsplit) (an item's sequence may fill fewer
+        // than the n_splits slots), recent ones [n_splits, S)
+        if (c0 + k < S && (c0 + k < nsplit || c0 + k >= rule.n_splits)) {
           lv[k] = load_agent(&part.l[base + c0 + k]);
           mv[k] = load_agent(&part.m[base + c0 + k]);
           ov[k] = load_agent2(&part.o[(base + c0 + k) * 128 + d]);
@@ -1143,6 +1182,96 @@ int launch_decode_order(const smaq_attn_params& p, int* order, hipStream_t st) {
   return launch_status("smaq_attn_hybrid(decode order)");
 }
 
+// Exclusive prefix sum over the kOrderBuckets threads of one workgroup
+// (Hillis-Steele in LDS); returns this thread's exclusive sum, and the total
+// in `total`.
+__device__ int block_exclusive_scan(int* buf, int v, int& total) {
+  const int tid = (int)__builtin_amdgcn_workitem_id_x();
+  buf[tid] = v;
+  for (int off = 1; off < kOrderBuckets; off <<= 1) {
+    __syncthreads();
+    const int add = tid >= off ? buf[tid - off] : 0;
+    __syncthreads();
+    buf[tid] += add;
+  }
+  __syncthreads();
+  total = buf[kOrderBuckets - 1];
+  const int ex = buf[tid] - v;
+  __syncthreads();
+  return ex;
+}
+
+// The longest-first schedule as work items.  Sequences are ranked longest
+// first by the same 1024 length buckets as decode_order_kernel.  Buckets
+// that begin within the first `first_round` ranks (the sequences whose KV
+// heads fill the first round of workgroup slots) run whole; every later
+// sequence runs in g pieces, g = ceil(L_hi / piece_len) capped at
+// max_pieces, L_hi the bucket's upper length bound, the boundaries at
+// L * k / g rounded down to whole 128-token steps.  A sequence's pieces
+// and boundaries thus follow from its length and the bucket counts alone
+// (not from the order within a bucket), so the merged output does not
+// depend on the schedule.  A sequence of rank r in bucket k takes items
+// r + E_k + (r - start_k) * (g_k - 1) ..., E_k the extra items of the
+// buckets before k; items past the last are written empty.
+__global__ __launch_bounds__(kOrderBuckets) void decode_items_kernel(
+    const long long* __restrict__ len, long long max_len, int batch, int first_round, int max_pieces,
+    long long piece_len, int n_items, DecodeItem* __restrict__ items) {
+  __shared__ int count[kOrderBuckets];
+  __shared__ int scan[kOrderBuckets];
+  const int tid = (int)__builtin_amdgcn_workitem_id_x();
+  count[tid] = 0;
+  __syncthreads();
+  auto clamp_len = [&](int b) {
+    long long L = len[b];
+    return L < 0 ? 0 : (L > max_len ? max_len : L);
+  };
+  auto bucket = [&](long long L) {
+    return kOrderBuckets - 1 - (int)(L * (kOrderBuckets - 1) / max_len);  // longest -> 0
+  };
+  for (int b = tid; b < batch; b += kOrderBuckets) atomicAdd(&count[bucket(clamp_len(b))], 1);
+  __syncthreads();
+  int total = 0;
+  const int c = count[tid];
+  const int start = block_exclusive_scan(scan, c, total);
+  // pieces of this bucket's sequences: lengths L with floor(L * 1023 / max)
+  // = j lie below (j + 1) * max / 1023
+  const long long j = kOrderBuckets - 1 - tid;
+  const long long hi = ((j + 1) * max_len + (kOrderBuckets - 2)) / (kOrderBuckets - 1);
+  long long g = (hi + piece_len - 1) / piece_len;
+  g = g < 1 ? 1 : (g > max_pieces ? max_pieces : g);
+  const int gk = start < first_round ? 1 : (int)g;
+  const int ek = block_exclusive_scan(scan, c * (gk - 1), total);
+  const int n_real = batch + total;  // items the lengths need (<= n_items)
+  __shared__ int start_of[kOrderBuckets], g_of[kOrderBuckets], e_of[kOrderBuckets];
+  count[tid] = start;  // the bucket's rank counter
+  start_of[tid] = start;
+  g_of[tid] = gk;
+  e_of[tid] = ek;
+  __syncthreads();
+  for (int b = tid; b < batch; b += kOrderBuckets) {
+    const long long L = clamp_len(b);
+    const int k = bucket(L);
+    const int r = atomicAdd(&count[k], 1);
+    const int gb = g_of[k];
+    const int base = r + e_of[k] + (r - start_of[k]) * (gb - 1);
+    long long t0 = 0;
+    for (int i = 0; i < gb; ++i) {
+      const long long t1 = i + 1 == gb ? L : (L * (i + 1) / gb) & ~127LL;
+      items[base + i] = DecodeItem{b, (int)t0, (int)t1, (gb << 16) | i};
+      t0 = t1;
+    }
+  }
+  for (int i = n_real + tid; i < n_items; i += kOrderBuckets) items[i] = DecodeItem{-1, 0, 0, 0};
+}
+
+int launch_decode_items(const smaq_attn_params& p, int first_round, int max_pieces, int64_t piece_len,
+                        int n_items, void* items, hipStream_t st) {
+  hipLaunchKernelGGL(decode_items_kernel, dim3(1), dim3(kOrderBuckets), 0, st, p.hist_len,
+                     (long long)p.max_hist_len, p.batch, first_round, max_pieces, (long long)piece_len,
+                     n_items, (DecodeItem*)items);
+  return launch_status("smaq_attn_hybrid(decode items)");
+}
+
 // Contexts are split so that the grid fills one round of the device's
 // workgroup slots (kDecodeWaves workgroups of 4 waves per CU): a workgroup's
 // fixed costs (its prologue and first tile's latency, the 4-wave merge) are
@@ -1172,8 +1301,9 @@ template <int KB, typename TN, bool SPLIT>
 static void launch_v(const smaq_attn_params& p, const HistAddr& a, const Partials& part, const SplitRule& rule,
                      int n_splits, const int* order, hipStream_t st) {
   // heads fastest, then sequences (the longest-first order when given), then
-  // splits: split-major, so that a one-round grid runs split s in round-slot s
-  dim3 grid(p.n_kv_heads, p.batch, n_splits);
+  // splits: split-major, so that a one-round grid runs split s in round-slot s;
+  // in item mode, heads fastest, then items
+  const dim3 grid(p.n_kv_heads, rule.pieces ? rule.items : p.batch, rule.pieces ? 1 : n_splits);
   switch (p.val_dtype) {
     case SMAQ_F32: hipLaunchKernelGGL((decode_mfma_kernel<KB, TN, float, SPLIT>), grid, dim3(256), 0, st, p, a, part, rule, order); break;
     case SMAQ_F16: hipLaunchKernelGGL((decode_mfma_kernel<KB, TN, _Float16, SPLIT>), grid, dim3(256), 0, st, p, a, part, rule, order); break;
@@ -1200,16 +1330,22 @@ static void launch_n(const smaq_attn_params& p, const HistAddr& a, const Partial
 }
 
 int launch_mfma_decode(const smaq_attn_params& p, const HistAddr& a, const Partials& part,
-                       int n_splits, bool direct, bool merge, const int* order, hipStream_t st) {
+                       int n_splits, bool direct, bool merge, const int* order, int items, hipStream_t st) {
   const bool wide = p.norm_dtype == SMAQ_F32 || p.val_dtype == SMAQ_F32;
   SplitRule rule;
   rule.n_splits = n_splits;
   rule.n_cu = device_cu_count();
   rule.slots = wide ? 3 : 4;
   rule.tilt = wide ? 0 : kSplitTilt4;
-  rule.direct = direct && n_splits == 1 ? 1 : 0;
-  rule.merge = merge && !rule.direct && p.arrivals ? 1 : 0;
+  rule.pieces = items > 0 ? 1 : 0;
+  rule.items = items;
+  // item mode: the sequences of one piece write the output when there is no
+  // recent part; the others merge their pieces (arrival counters required)
+  rule.direct = direct && (rule.pieces || n_splits == 1) ? 1 : 0;
+  rule.merge = merge && p.arrivals && (rule.pieces || !rule.direct) ? 1 : 0;
   SMAQ_REQUIRE(!rule.merge || part.S >= n_splits, "smaq_attn_hybrid: merge partials missing");
+  SMAQ_REQUIRE(!rule.pieces || (order && rule.merge && n_splits <= 0xffff),
+               "smaq_attn_hybrid: decode pieces need items and arrival counters");
   if (p.key_bits == 3) launch_n<3>(p, a, part, rule, n_splits, order, st);
   else launch_n<4>(p, a, part, rule, n_splits, order, st);
   return launch_status("smaq_attn_hybrid(mfma decode)");

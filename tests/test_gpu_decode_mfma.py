@@ -190,6 +190,155 @@ def test_mfma_decode_paged_longest_first(dev):
     assert_attn_close(out[200:201], v_hat.unsqueeze(0).bfloat16(), "longest first seq 200 len 1")
 
 
+def _paged_table(lens, bs, gen, spare=7):
+    nblk = [(n + bs - 1) // bs for n in lens]
+    nphys = sum(nblk) + spare
+    perm = torch.randperm(nphys, generator=gen)
+    table = torch.zeros(len(lens), max(nblk), dtype=torch.int32)
+    o = 0
+    for b, nb in enumerate(nblk):
+        table[b, :nb] = perm[o:o + nb].to(torch.int32)
+        o += nb
+    return table, nphys
+
+
+def _first_round(dev, hkv):
+    """Sequences whose KV heads fill one round of decode workgroup slots (4
+    per CU with 16-bit metadata)."""
+    return torch.cuda.get_device_properties(dev).multi_processor_count * 4 // hkv
+
+
+def _item_rows(plan, B, hkv):
+    """The work items the library wrote into the plan's workspace (after the
+    partials): [n_items, 4] int32 rows (sequence, first token, end token,
+    count << 16 | piece)."""
+    fr = _first_round(plan.device, hkv)
+    n_items = fr + (B - fr) * _max_pieces(plan)
+    off = plan.workspace.numel() - n_items * 16
+    return plan.workspace[off:].view(torch.int32).view(n_items, 4).cpu(), n_items
+
+
+PIECE_TOKENS = 4096  # the library's kDecodePiece (attention.hip)
+
+
+def _max_pieces(plan):
+    """Pieces the plan allows per sequence: pieces of the history length over
+    8, at least PIECE_TOKENS, rounded up to 128-token steps."""
+    L = plan.params.max_hist_len
+    piece = max(PIECE_TOKENS, -(-L // 8))
+    piece = -(-piece // 128) * 128
+    return -(-L // piece)
+
+
+def test_mfma_decode_paged_pieces(dev):
+    """More ragged sequences than one round of workgroup slots holds (192 x 8
+    KV heads against 1,024 slots) and histories above 4,096 tokens: the
+    sequences that start after the first round run in pieces of about 4,096
+    tokens, merged by the decode kernel's arrival counters.  The library's
+    item list covers every sequence's history exactly once, within the
+    planned number of items and pieces; the output is the same bits on a
+    second call (counters reset), matches the generic kernels for every
+    sequence, and the oracle for the longest sequence and pieced ones."""
+    strat, codec = _codec_pair(dev, 3, 380)
+    gen = torch.Generator().manual_seed(381)
+    B, bs, hkv = 192, 16, 8
+    lens = [int(x) for x in torch.randint(4200, 4701, (B,), generator=gen)]
+    lens[5] = 9000
+    table, nphys = _paged_table(lens, bs, gen)
+    allk = sample_keys(sum(lens) * hkv, seed=382).reshape(sum(lens), hkv, 128).bfloat16()
+    allv = torch.randn(sum(lens), hkv, 128, generator=gen).bfloat16()
+    cut = [0]
+    for n in lens:
+        cut.append(cut[-1] + n)
+    keys = [allk[cut[b]:cut[b + 1]] for b in range(B)]
+    vals = [allv[cut[b]:cut[b + 1]] for b in range(B)]
+    pk = PagedQuantizedKV.encode(strat, [k.to(dev) for k in keys], [v.to(dev) for v in vals], table.to(dev),
+                                 num_blocks=nphys, block_size=bs)
+    del allk, allv
+    q = torch.randn(B, 32, 128, generator=gen).bfloat16()
+    plan = pk.plan(q.to(dev), impl=2)
+    maxp = _max_pieces(plan)
+    assert maxp == 3
+    partials = B * hkv * 4 * maxp * (128 + 2) * 4
+    fr = _first_round(dev, hkv)
+    assert fr < B - 32, f"the test needs more sequences than the first round ({fr})"
+    n_items = fr + (B - fr) * maxp
+    assert plan.workspace.numel() == ((partials + 255) // 256) * 256 + n_items * 16, "pieces not planned"
+    out = plan.run(q.to(dev)).squeeze(1).clone()
+    again = plan.run(q.to(dev)).squeeze(1)
+    torch.cuda.synchronize()
+    assert torch.equal(out, again), "second call differs"
+    assert int(plan.arrivals.abs().sum()) == 0, "arrival counters not reset"
+    items, _ = _item_rows(plan, B, hkv)
+    real = items[items[:, 0] >= 0]
+    assert bool((items[len(real):, 0] < 0).all()), "empty items must follow the real ones"
+    pieced = set()
+    for b in range(B):
+        rows = real[real[:, 0] == b]
+        count = int(rows[0, 3]) >> 16
+        assert 1 <= count <= maxp and len(rows) == count, f"seq {b}: {len(rows)} items, count {count}"
+        rows = rows[torch.argsort(rows[:, 3] & 0xFFFF)]
+        assert int(rows[0, 1]) == 0 and int(rows[-1, 2]) == lens[b], f"seq {b} range"
+        assert bool((rows[1:, 1] == rows[:-1, 2]).all()), f"seq {b} pieces not contiguous"
+        assert bool((rows[:-1, 2] % 128 == 0).all()), f"seq {b} boundaries off the 128-token step"
+        if count > 1:
+            pieced.add(b)
+    assert len(pieced) >= 32, f"only {len(pieced)} sequences pieced"
+    order = sorted(range(B), key=lambda b: -lens[b])
+    assert not (pieced & set(order[:fr])), "a first-round sequence was pieced"
+    out_g = pk.attention(q.to(dev), impl=1)
+    assert_attn_close(out, out_g.cpu(), "pieces vs generic (all sequences)")
+    for b in [5] + sorted(pieced)[:3]:
+        assert_attn_close(out[b:b + 1], _oracle(codec, keys[b], vals[b], q[b:b + 1], 32, hkv),
+                          f"pieces seq {b} len {lens[b]}")
+
+
+@pytest.mark.parametrize("odtype", [torch.bfloat16, torch.float32])
+def test_mfma_decode_pieces_with_recent(dev, odtype):
+    """Longest-first pieces on a contiguous ragged batch with an exact recent
+    window (per-sequence lengths, some empty): the recent phase runs first,
+    the decode kernel's last workgroup per (sequence, KV head) merges its
+    pieces and the recent partials.  Same bits on a second call; the generic
+    kernels for every sequence and the oracle on a sample."""
+    strat, codec = _codec_pair(dev, 3, 390)
+    gen = torch.Generator().manual_seed(391)
+    B, hkv, g, RW = 160, 8, 4, 24
+    lens = [int(x) for x in torch.randint(4200, 5001, (B,), generator=gen)]
+    rl = [int(x) for x in torch.randint(0, RW + 1, (B,), generator=gen)]
+    allk = sample_keys(sum(lens) * hkv, seed=392).reshape(sum(lens), hkv, 128).bfloat16()
+    allv = torch.randn(sum(lens), hkv, 128, generator=gen).bfloat16()
+    cut = [0]
+    for n in lens:
+        cut.append(cut[-1] + n)
+    keys = [allk[cut[b]:cut[b + 1]] for b in range(B)]
+    vals = [allv[cut[b]:cut[b + 1]] for b in range(B)]
+    kvb = QuantizedKVBatch.encode(strat, [k.to(dev) for k in keys], [v.to(dev) for v in vals])
+    del allk, allv
+    rk = torch.randn(B, RW, hkv, 128, generator=gen).bfloat16()
+    rv = torch.randn(B, RW, hkv, 128, generator=gen).bfloat16()
+    q = torch.randn(B, hkv * g, 128, generator=gen).to(odtype)
+    qd = q.to(dev)
+    plan = kvb.plan(qd, recent_k=rk.to(dev), recent_v=rv.to(dev), recent_len=torch.tensor(rl), impl=2)
+    maxp = _max_pieces(plan)
+    assert maxp == 2
+    out = plan.run(qd).squeeze(1).clone()
+    again = plan.run(qd).squeeze(1).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(out, again) and int(plan.arrivals.abs().sum()) == 0
+    items, _ = _item_rows(plan, B, hkv)
+    counts = items[items[:, 0] >= 0, 3] >> 16
+    assert int(counts.max()) >= 2, "no sequence pieced"
+    out_g = kvb.attention(qd, recent_k=rk.to(dev), recent_v=rv.to(dev), recent_len=torch.tensor(rl), impl=1)
+    assert_attn_close(out, out_g.cpu(), f"pieces + recent vs generic {odtype}")
+    short = sorted(range(B), key=lambda b: lens[b])
+    for b in short[:2] + [short[-1]]:
+        st = R.Store(codec, 128, hkv)
+        st.append_chunk(keys[b], vals[b])
+        n = rl[b]
+        want = R.hybrid_attention(q[b:b + 1], st, rk[b, :n] if n else None, rv[b, :n] if n else None, hkv * g)
+        assert_attn_close(out[b:b + 1], want, f"pieces + recent {odtype} seq {b}")
+
+
 def test_mfma_decode_peaked_scores(dev):
     """Large query norms (sharp softmax): the hi/lo splits keep scores exact
     enough that the winning tokens' weights match."""

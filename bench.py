@@ -310,9 +310,8 @@ def bench_paged(args, dev):
     token_heads = int(lens.sum()) * Hkv
     algo = token_heads * pk.nbytes_per_token_head()
     ms_step, st = time_steps(lambda: plan.run(q), args)
-    plan.load_query(q)
-    plan.launch(phases=8)    # the query rotation, once: the timed launches are the decode kernel alone
-    kern = kernel_ms(lambda: plan.launch(phases=1), args.steps)
+    plan.run(q)   # rotation and longest-first schedule, once: the timed launches are the decode kernel alone
+    kern = kernel_ms(lambda: plan.launch(phases=1 | 16), args.steps)
     achieved = algo / (kern * 1e-3) / 1e9
     cpu = None if args.no_cpu_baseline else cpu_baseline_paged(strat, table, lens, bs, codes, norms, vd, vsc, vz,
                                                                   q, Hq, Hkv, D)

@@ -265,7 +265,10 @@ typedef struct smaq_attn_params {
      writes the output itself and phase 4 launches nothing; with arrival
      counters (below) it merges several splits itself, and, when one call
      launches phases 1 and 2, the recent partials too (the recent phase then
-     runs first). */
+     runs first).  For ragged batches that kernel runs in a longest-first
+     schedule which phase 1 builds first (one small launch); with 16 added,
+     phase 1 reuses the schedule an earlier call on this workspace built for
+     the same lengths, so the decode kernel can be timed alone. */
   int phases;
   /* kernel choice: 0 = automatic (matrix-core decode kernel when the shape
      allows, generic kernels otherwise), 1 = generic kernels only, 2 = the

@@ -718,9 +718,10 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
                p.block_size, p.n_kv_heads};
     int rc = SMAQ_EUNSUPPORTED;
     if (pl.mfma) {
-      int* order = nullptr;
-      if (pl.longest_first) {
-        order = (int*)((char*)p.workspace + align256(partial_bytes(&p, pl)));
+      // the longest-first schedule (order or work items), unless phase 16
+      // keeps the one an earlier call built
+      int* order = pl.longest_first ? (int*)((char*)p.workspace + align256(partial_bytes(&p, pl))) : nullptr;
+      if (pl.longest_first && !(phases & 16)) {
         rc = pl.n_items > 0
                  ? launch_decode_items(p, pl.first_round, pl.s_hist, pl.piece_len, pl.n_items, order, st)
                  : launch_decode_order(p, order, st);

@@ -114,11 +114,18 @@ int64_t mfma_decode_split_len(const smaq_attn_params& p);
 // order their workgroups are dispatched; launch_decode_order fills it with
 // the sequences by history length, longest first.
 int launch_decode_order(const smaq_attn_params& p, int* order, hipStream_t st);
-// The longest-first order as `n_items` work items (16 bytes each, at
-// `items`): the sequences ranked first_round and later run in up to
-// max_pieces pieces of about piece_len tokens.
+// A work item of the longest-first piece schedule: tokens [t0, t1) of
+// sequence seq, piece `meta & 0xffff` of `meta >> 16`.  seq < 0: no work
+// (the decode grid is sized for the most items the lengths could need).
+struct DecodeItem {
+  int seq, t0, t1, meta;
+};
+// The longest-first order as `n_items` work items (at `items`): the
+// sequences ranked first_round and later run in up to max_pieces pieces of
+// about piece_len tokens (decode_schedule.hip).
 int launch_decode_items(const smaq_attn_params& p, int first_round, int max_pieces, int64_t piece_len,
                         int n_items, void* items, hipStream_t st);
+
 // With `direct` (one split and no recent part) the kernel writes the final
 // output itself, and no split combine is needed; with `merge` (several
 // splits, no recent part, p.arrivals set) the last workgroup of each

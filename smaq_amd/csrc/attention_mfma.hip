@@ -85,12 +85,6 @@ struct SplitRule {
   int items;  // grid rows in item mode
 };
 
-// A work item of the longest-first piece schedule: tokens [t0, t1) of
-// sequence seq, piece `piece` of `count`.  seq < 0: no work (the grid is
-// sized for the most items the lengths could need).
-struct DecodeItem {
-  int seq, t0, t1, meta;  // meta = count << 16 | piece
-};
 constexpr int kSplitWeight = 64;
 
 // The splits of unit u (of `units`) from which on the round-slot is at
@@ -1140,136 +1134,6 @@ bool mfma_decode_supported(const smaq_attn_params& p) {
          // aligned arrays
          (((uintptr_t)p.key_bytes | (uintptr_t)p.val_bytes | (uintptr_t)p.key_norms |
            (uintptr_t)p.val_scales | (uintptr_t)p.val_zeros | (uintptr_t)p.q_hist) & 15) == 0;
-}
-
-// Sequences by history length, longest first: a counting sort on 1024
-// length buckets by one workgroup (bucket order is deterministic; the order
-// within a bucket is not, and does not change any result: each workgroup
-// computes its own (sequence, head) partials).
-constexpr int kOrderBuckets = 1024;
-
-__global__ __launch_bounds__(kOrderBuckets) void decode_order_kernel(const long long* __restrict__ len,
-                                                                     long long max_len, int batch,
-                                                                     int* __restrict__ order) {
-  __shared__ int count[kOrderBuckets];
-  const int tid = (int)__builtin_amdgcn_workitem_id_x();
-  count[tid] = 0;
-  __syncthreads();
-  auto bucket = [&](int b) {
-    long long L = len[b];
-    L = L < 0 ? 0 : (L > max_len ? max_len : L);
-    return kOrderBuckets - 1 - (int)(L * (kOrderBuckets - 1) / max_len);  // longest -> 0
-  };
-  for (int b = tid; b < batch; b += kOrderBuckets) atomicAdd(&count[bucket(b)], 1);
-  __syncthreads();
-  // exclusive prefix sum of the counts (Hillis-Steele over the workgroup)
-  int v = count[tid];
-  for (int off = 1; off < kOrderBuckets; off <<= 1) {
-    __syncthreads();
-    const int add = tid >= off ? count[tid - off] : 0;
-    __syncthreads();
-    count[tid] += add;
-  }
-  __syncthreads();
-  count[tid] -= v;  // inclusive -> exclusive
-  __syncthreads();
-  for (int b = tid; b < batch; b += kOrderBuckets) order[atomicAdd(&count[bucket(b)], 1)] = b;
-}
-
-int launch_decode_order(const smaq_attn_params& p, int* order, hipStream_t st) {
-  hipLaunchKernelGGL(decode_order_kernel, dim3(1), dim3(kOrderBuckets), 0, st, p.hist_len,
-                     (long long)p.max_hist_len, p.batch, order);
-  return launch_status("smaq_attn_hybrid(decode order)");
-}
-
-// Exclusive prefix sum over the kOrderBuckets threads of one workgroup
-// (Hillis-Steele in LDS); returns this thread's exclusive sum, and the total
-// in `total`.
-__device__ int block_exclusive_scan(int* buf, int v, int& total) {
-  const int tid = (int)__builtin_amdgcn_workitem_id_x();
-  buf[tid] = v;
-  for (int off = 1; off < kOrderBuckets; off <<= 1) {
-    __syncthreads();
-    const int add = tid >= off ? buf[tid - off] : 0;
-    __syncthreads();
-    buf[tid] += add;
-  }
-  __syncthreads();
-  total = buf[kOrderBuckets - 1];
-  const int ex = buf[tid] - v;
-  __syncthreads();
-  return ex;
-}
-
-// The longest-first schedule as work items.  Sequences are ranked longest
-// first by the same 1024 length buckets as decode_order_kernel.  Buckets
-// that begin within the first `first_round` ranks (the sequences whose KV
-// heads fill the first round of workgroup slots) run whole; every later
-// sequence runs in g pieces, g = ceil(L_hi / piece_len) capped at
-// max_pieces, L_hi the bucket's upper length bound, the boundaries at
-// L * k / g rounded down to whole 128-token steps.  A sequence's pieces
-// and boundaries thus follow from its length and the bucket counts alone
-// (not from the order within a bucket), so the merged output does not
-// depend on the schedule.  A sequence of rank r in bucket k takes items
-// r + E_k + (r - start_k) * (g_k - 1) ..., E_k the extra items of the
-// buckets before k; items past the last are written empty.
-__global__ __launch_bounds__(kOrderBuckets) void decode_items_kernel(
-    const long long* __restrict__ len, long long max_len, int batch, int first_round, int max_pieces,
-    long long piece_len, int n_items, DecodeItem* __restrict__ items) {
-  __shared__ int count[kOrderBuckets];
-  __shared__ int scan[kOrderBuckets];
-  const int tid = (int)__builtin_amdgcn_workitem_id_x();
-  count[tid] = 0;
-  __syncthreads();
-  auto clamp_len = [&](int b) {
-    long long L = len[b];
-    return L < 0 ? 0 : (L > max_len ? max_len : L);
-  };
-  auto bucket = [&](long long L) {
-    return kOrderBuckets - 1 - (int)(L * (kOrderBuckets - 1) / max_len);  // longest -> 0
-  };
-  for (int b = tid; b < batch; b += kOrderBuckets) atomicAdd(&count[bucket(clamp_len(b))], 1);
-  __syncthreads();
-  int total = 0;
-  const int c = count[tid];
-  const int start = block_exclusive_scan(scan, c, total);
-  // pieces of this bucket's sequences: lengths L with floor(L * 1023 / max)
-  // = j lie below (j + 1) * max / 1023
-  const long long j = kOrderBuckets - 1 - tid;
-  const long long hi = ((j + 1) * max_len + (kOrderBuckets - 2)) / (kOrderBuckets - 1);
-  long long g = (hi + piece_len - 1) / piece_len;
-  g = g < 1 ? 1 : (g > max_pieces ? max_pieces : g);
-  const int gk = start < first_round ? 1 : (int)g;
-  const int ek = block_exclusive_scan(scan, c * (gk - 1), total);
-  const int n_real = batch + total;  // items the lengths need (<= n_items)
-  __shared__ int start_of[kOrderBuckets], g_of[kOrderBuckets], e_of[kOrderBuckets];
-  count[tid] = start;  // the bucket's rank counter
-  start_of[tid] = start;
-  g_of[tid] = gk;
-  e_of[tid] = ek;
-  __syncthreads();
-  for (int b = tid; b < batch; b += kOrderBuckets) {
-    const long long L = clamp_len(b);
-    const int k = bucket(L);
-    const int r = atomicAdd(&count[k], 1);
-    const int gb = g_of[k];
-    const int base = r + e_of[k] + (r - start_of[k]) * (gb - 1);
-    long long t0 = 0;
-    for (int i = 0; i < gb; ++i) {
-      const long long t1 = i + 1 == gb ? L : (L * (i + 1) / gb) & ~127LL;
-      items[base + i] = DecodeItem{b, (int)t0, (int)t1, (gb << 16) | i};
-      t0 = t1;
-    }
-  }
-  for (int i = n_real + tid; i < n_items; i += kOrderBuckets) items[i] = DecodeItem{-1, 0, 0, 0};
-}
-
-int launch_decode_items(const smaq_attn_params& p, int first_round, int max_pieces, int64_t piece_len,
-                        int n_items, void* items, hipStream_t st) {
-  hipLaunchKernelGGL(decode_items_kernel, dim3(1), dim3(kOrderBuckets), 0, st, p.hist_len,
-                     (long long)p.max_hist_len, p.batch, first_round, max_pieces, (long long)piece_len,
-                     n_items, (DecodeItem*)items);
-  return launch_status("smaq_attn_hybrid(decode items)");
 }
 
 // Contexts are split so that the grid fills one round of the device's

@@ -216,7 +216,9 @@ class AttentionPlan:
 
     def launch(self, phases: int = 0) -> torch.Tensor:
         """Launch the attention phases on the current stream: 0 = all, else a
-        mask of 8 (query rotation), 1 (history), 2 (recent), 4 (combine)."""
+        mask of 8 (query rotation), 1 (history), 2 (recent), 4 (combine), and
+        16 (the history phase reuses the decode schedule an earlier call built
+        for the same lengths: the decode kernel alone)."""
         self.params.phases = phases
         _native.attn_hybrid(self.params, self.device)
         return self.out

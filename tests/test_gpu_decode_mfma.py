@@ -269,6 +269,19 @@ def test_mfma_decode_paged_pieces(dev):
     torch.cuda.synchronize()
     assert torch.equal(out, again), "second call differs"
     assert int(plan.arrivals.abs().sum()) == 0, "arrival counters not reset"
+    # the rotation alone, then the history phase (schedule launch + decode),
+    # and the decode kernel alone on that schedule (phase 16) give the same
+    # bits as the full call
+    plan.load_query(q.to(dev))
+    plan.out.zero_()
+    plan.launch(phases=8)
+    plan.launch(phases=1)
+    torch.cuda.synchronize()
+    assert torch.equal(plan.out.squeeze(1), out), "separate rotation and schedule launches differ"
+    plan.out.zero_()
+    plan.launch(phases=1 | 16)
+    torch.cuda.synchronize()
+    assert torch.equal(plan.out.squeeze(1), out), "decode on the kept schedule differs"
     items, _ = _item_rows(plan, B, hkv)
     real = items[items[:, 0] >= 0]
     assert bool((items[len(real):, 0] < 0).all()), "empty items must follow the real ones"

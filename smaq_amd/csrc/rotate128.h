@@ -18,7 +18,7 @@
 namespace smaq {
 
 template <int ROWS>
-struct Rot128Lds {
+struct __attribute__((aligned(16))) Rot128Lds {  // 16-byte LDS accesses
   float xs[ROWS][128];
   float part[ROWS][8][128];
 };
@@ -43,10 +43,34 @@ __device__ __forceinline__ void rotate128_block(Rot128Lds<ROWS>& L, const void* 
   float4 m[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) m[i] = *(const float4*)(Mt + (16 * dq + i) * 128 + 4 * cg);
+  if (((uintptr_t)x & 15) == 0 && xdtype != SMAQ_F32) {
+    // 16-byte loads of 8 fp16 / bf16 elements (c5's 8192 rows: 13.0 -> 10.0 us
+    // with 8-row blocks; the same values as element loads)
 #pragma unroll
-  for (int e = t; e < ROWS * 128; e += 256) {
-    const int64_t r = r0 + e / 128;
-    L.xs[e / 128][e % 128] = r < rows ? query_elem(x, xdtype, r * 128 + e % 128) : 0.0f;
+    for (int e = 8 * t; e < ROWS * 128; e += 8 * 256) {
+      const int64_t r = r0 + e / 128;
+      const uint4 w = r < rows ? *(const uint4*)((const uint16_t*)x + r * 128 + e % 128) : make_uint4(0, 0, 0, 0);
+      const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const uint16_t h = (uint16_t)(wd[k >> 1] >> (16 * (k & 1)));
+        L.xs[e / 128][e % 128 + k] = xdtype == SMAQ_F16 ? Num<_Float16>::to_f(__builtin_bit_cast(_Float16, h))
+                                                        : Num<bf16>::to_f(__builtin_bit_cast(bf16, h));
+      }
+    }
+  } else if (((uintptr_t)x & 15) == 0) {
+#pragma unroll
+    for (int e = 4 * t; e < ROWS * 128; e += 4 * 256) {
+      const int64_t r = r0 + e / 128;
+      const float4 w = r < rows ? *(const float4*)((const float*)x + r * 128 + e % 128) : make_float4(0, 0, 0, 0);
+      *(float4*)&L.xs[e / 128][e % 128] = w;
+    }
+  } else {
+#pragma unroll
+    for (int e = t; e < ROWS * 128; e += 256) {
+      const int64_t r = r0 + e / 128;
+      L.xs[e / 128][e % 128] = r < rows ? query_elem(x, xdtype, r * 128 + e % 128) : 0.0f;
+    }
   }
   __syncthreads();
 #pragma unroll 2
@@ -74,7 +98,9 @@ __device__ __forceinline__ void rotate128_block(Rot128Lds<ROWS>& L, const void* 
 }
 
 // blocks of 4 rows up to this many rows (a c3 step's 1024 rows: 256 blocks),
-// 16 beyond (fewer copies of the 64 KB matrix read from L2)
+// 8 beyond (fewer copies of the 64 KB matrix read from L2, and still one
+// round of blocks at c5's 8192 rows: 10.0 us against 10.3 with 16 rows and
+// 10.9 with 4, timed after a 512 MB read sweep)
 constexpr int64_t kRot128ManyRows = 2048;
 
 }  // namespace smaq

@@ -305,15 +305,15 @@ extern "C" int smaq_rotate_rows(const void* x, int xdtype, long long rows, int D
   SMAQ_REQUIRE(blocks < (1ll << 31), "smaq_rotate_rows: too many rows");
   hipStream_t st = (hipStream_t)stream;
   if (D == 128 && ((uintptr_t)Mt & 15) == 0) {  // (16-byte loads of Mt)
-    const int rpb = rows > kRot128ManyRows ? 16 : 4;
+    const int rpb = rows > kRot128ManyRows ? 8 : 4;
     SMAQ_REQUIRE((rows + rpb - 1) / rpb < (1ll << 31), "smaq_rotate_rows: too many rows");
     const dim3 grid((unsigned)((rows + rpb - 1) / rpb));
     if (xdtype != SMAQ_F32 && xdtype != SMAQ_F16 && xdtype != SMAQ_BF16) {
       set_error("smaq_rotate_rows: unsupported dtype %d", xdtype);
       return SMAQ_EUNSUPPORTED;
     }
-    if (rpb == 16)
-      hipLaunchKernelGGL(rotate_rows128_kernel<16>, grid, dim3(256), 0, st, x, xdtype, (int64_t)rows, Mt,
+    if (rpb == 8)
+      hipLaunchKernelGGL(rotate_rows128_kernel<8>, grid, dim3(256), 0, st, x, xdtype, (int64_t)rows, Mt,
                          coord_scales, out);
     else
       hipLaunchKernelGGL(rotate_rows128_kernel<4>, grid, dim3(256), 0, st, x, xdtype, (int64_t)rows, Mt,

@@ -186,16 +186,17 @@ def test_scalar_dequant_scores_rotate(dev):
     torch.testing.assert_close(raw.cpu(), R.smaq_scores(query[0], ref, c, Ei, 128), atol=2e-3, rtol=1e-4)
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("scaled", [False, True])
 def test_rotate_rows_128_chunking_and_accuracy(dev, dtype, scaled):
     """smaq_rotate_rows at head_dim 128 (the decode query rotation): each
     output is eight 16-term fmaf chains summed in a fixed tree, an order set
-    by the row alone, so 5001 rows in one call (16-row blocks, the last one
+    by the row alone, so 5001 rows in one call (8-row blocks, the last one
     partial) equal the same rows in calls of 301 (4-row blocks), 2499 and
-    2201 rows bit for bit, and match the float64 product within the rounding
-    bound of a 20-step fp32 evaluation (16 chained products, 3 tree levels,
-    the scale)."""
+    2201 rows, and rows read from a buffer that is not 16-byte aligned
+    (element loads instead of 16-byte loads), bit for bit, and match the
+    float64 product within the rounding bound of a 20-step fp32 evaluation
+    (16 chained products, 3 tree levels, the scale)."""
     g = torch.Generator().manual_seed(130)
     M = torch.linalg.qr(torch.randn(128, 128, generator=g, dtype=torch.float64))[0].float()
     cs = (torch.rand(128, generator=g) + 0.5) if scaled else None
@@ -209,6 +210,13 @@ def test_rotate_rows_128_chunking_and_accuracy(dev, dtype, scaled):
     _native.rotate_rows_into(xd[301:2800], Mt, csd, parts[301:2800])
     _native.rotate_rows_into(xd[2800:], Mt, csd, parts[2800:])
     assert torch.equal(whole, parts)
+    buf = torch.empty(5001 * 128 + 1, dtype=dtype, device=dev)
+    xm = buf[1:].view(5001, 128)
+    xm.copy_(xd)
+    assert xm.data_ptr() % 16 != 0
+    odd = torch.empty(5001, 128, device=dev)
+    _native.rotate_rows_into(xm, Mt, csd, odd)
+    assert torch.equal(whole, odd)
     ref = x.double() @ M.T.double()
     if cs is not None:
         ref = ref * cs.double()

@@ -268,7 +268,8 @@ typedef struct smaq_attn_params {
      runs first).  For ragged batches that kernel runs in a longest-first
      schedule which phase 1 builds first (one small launch); with 16 added,
      phase 1 reuses the schedule an earlier call on this workspace built for
-     the same lengths, so the decode kernel can be timed alone. */
+     the same lengths, so the decode kernel can be timed alone (with any
+     other workspace contents the output is undefined). */
   int phases;
   /* kernel choice: 0 = automatic (matrix-core decode kernel when the shape
      allows, generic kernels otherwise), 1 = generic kernels only, 2 = the

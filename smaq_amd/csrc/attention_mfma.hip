@@ -399,13 +399,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
     const ConstIntPtr it = (ConstIntPtr)order + 4 * __builtin_amdgcn_readfirstlane(osel);
     const int seq = it[0], t0 = it[1], t1 = it[2], meta = it[3];  // one 16-byte scalar load
     b = __builtin_amdgcn_readfirstlane(seq);
-    if (b < 0) return;  // no work (uniform over the workgroup)
-    s0 = __builtin_amdgcn_readfirstlane(t0);
-    s1 = __builtin_amdgcn_readfirstlane(t1);
-    s = __builtin_amdgcn_readfirstlane(meta & 0xffff);
+    // b < 0: no work (uniform over the workgroup).  The range checks keep a
+    // stale schedule (phase 16 on a workspace the lengths no longer match)
+    // inside the buffers; its results are then undefined.
+    if ((unsigned)b >= (unsigned)p.batch) return;
+    s1 = min((int64_t)__builtin_amdgcn_readfirstlane(t1), p.max_hist_len);
+    s0 = min((int64_t)__builtin_amdgcn_readfirstlane(t0), s1);
+    s0 = s0 < 0 ? 0 : s0;
     nsplit = __builtin_amdgcn_readfirstlane(meta >> 16);
+    nsplit = nsplit < 1 ? 1 : (nsplit > rule.n_splits ? rule.n_splits : nsplit);
+    s = __builtin_amdgcn_readfirstlane(meta & 0xffff);
+    s = s < nsplit ? s : nsplit - 1;
   } else {
     b = order ? ((ConstIntPtr)order)[__builtin_amdgcn_readfirstlane(osel)] : gy;
+    if (order && (unsigned)b >= (unsigned)p.batch) return;  // a stale order (as above)
     s = gz;
     nsplit = rule.n_splits;
   }
@@ -475,6 +482,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
   const int bsz = addr.block_size;          // a power of two (checked on the host)
   const int n_kv = addr.n_kv;
   const int bshift = __builtin_ctz((unsigned)bsz);
+  if (rule.pieces && paged) {
+    // (a stale item's range stays inside the block-table row)
+    s1 = uniform64(min(s1, (int64_t)addr.max_blocks << bshift));
+    s0 = uniform64(min(s0, s1));
+  }
   auto group_row = [&](int64_t t0g) -> int64_t {
     if (!paged) return contig_base + t0g;
     const uint32_t tg = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)t0g);

@@ -266,7 +266,8 @@ typedef struct smaq_attn_params {
      counters (below) it merges several splits itself, and, when one call
      launches phases 1 and 2, the recent partials too (the recent phase then
      runs first).  For ragged batches that kernel runs in a longest-first
-     schedule which phase 1 builds first (one small launch); with 16 added,
+     schedule which phase 1 builds first (inside the rotation's launch when
+     phases 8 and 1 run in one call); with 16 added,
      phase 1 reuses the schedule an earlier call on this workspace built for
      the same lengths, so the decode kernel can be timed alone (with any
      other workspace contents the output is undefined). */

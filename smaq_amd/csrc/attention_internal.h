@@ -125,6 +125,13 @@ struct DecodeItem {
 // about piece_len tokens (decode_schedule.hip).
 int launch_decode_items(const smaq_attn_params& p, int first_round, int max_pieces, int64_t piece_len,
                         int n_items, void* items, hipStream_t st);
+// One launch for the query rotation (p.q_raw by p.rot_mt into p.q_hist, as
+// smaq_rotate_rows at head_dim 128) and the decode schedule: the order at
+// `sched` when n_items is 0, else the work items.  Supported at head_dim 128
+// with a 16-byte aligned rot_mt and a raw fp32/fp16/bf16 query.
+bool rotate_schedule_supported(const smaq_attn_params& p);
+int launch_rotate_schedule(const smaq_attn_params& p, int first_round, int max_pieces, int64_t piece_len,
+                           int n_items, void* sched, hipStream_t st);
 
 // With `direct` (one split and no recent part) the kernel writes the final
 // output itself, and no split combine is needed; with `merge` (several

@@ -274,9 +274,9 @@ def test_mfma_decode_paged_pieces(dev, bs, dtype):
     torch.cuda.synchronize()
     assert torch.equal(out, again), "second call differs"
     assert int(plan.arrivals.abs().sum()) == 0, "arrival counters not reset"
-    # the rotation alone, then the history phase (schedule launch + decode),
-    # and the decode kernel alone on that schedule (phase 16) give the same
-    # bits as the full call
+    # the full call builds the schedule inside the rotation's launch; the
+    # rotation alone, then the history phase (schedule launch + decode), and
+    # the decode kernel alone on that schedule (phase 16) give the same bits
     plan.load_query(q.to(dev))
     plan.out.zero_()
     plan.launch(phases=8)

@@ -517,11 +517,13 @@ static Plan make_plan(const smaq_attn_params* p) {
     piece = piece < kDecodePiece ? kDecodePiece : piece;
     piece = (piece + step - 1) / step * step;
     const int max_pieces = (int)((hl + piece - 1) / piece);
-    if (p->batch > first_round && max_pieces >= 2) {
+    // (the items are the decode grid's y dimension, at most 65535)
+    const int64_t items = first_round + (int64_t)(p->batch - first_round) * max_pieces;
+    if (p->batch > first_round && max_pieces >= 2 && items <= 65535) {
       pl.first_round = first_round;
       pl.piece_len = piece;
       pl.s_hist = max_pieces;
-      pl.n_items = first_round + (p->batch - first_round) * max_pieces;
+      pl.n_items = (int)items;
     }
   }
   return pl;

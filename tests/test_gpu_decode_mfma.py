@@ -311,6 +311,36 @@ def test_mfma_decode_paged_pieces(dev, bs, dtype):
                           f"pieces seq {b} len {lens[b]}")
 
 
+@pytest.mark.parametrize("max_len,pieced", [(16384, True), (32768, False)])
+def test_decode_pieces_plan_respects_the_grid_limit(dev, max_len, pieced):
+    """The work items are the decode grid's y dimension (at most 65535): a
+    paged batch of 10,000 ragged sequences takes pieces while first round +
+    later sequences x most pieces fits (histories up to 16,384 tokens: 4
+    pieces), and the one-split longest-first order beyond (32,768: 8 pieces
+    would need 79,104 items).  Only the workspace size is asked for (the
+    parameter block's pointers are placeholders the size computation does
+    not read)."""
+    from smaq_amd import _native
+    _native.lib()  # the library on this device
+    B, hkv, hq = 10000, 8, 32
+    p = _native.AttnParams()
+    p.batch, p.q_len, p.n_q_heads, p.n_kv_heads, p.head_dim, p.scale = B, 1, hq, hkv, 128, 128 ** -0.5
+    fake = 1 << 20  # 16-byte aligned placeholders
+    p.q_hist = p.q_exact = p.out = p.workspace = p.key_lut = fake
+    p.has_history, p.key_format, p.key_bits, p.key_row_bytes = 1, _native.KEY_SCALAR, 3, 64
+    p.key_bytes = p.key_norms = p.val_bytes = p.val_scales = p.val_zeros = fake
+    p.norm_dtype = p.val_dtype = p.out_dtype = _native.dtype_code(torch.bfloat16)
+    p.val_bits, p.val_group, p.val_row_bytes = 2, 32, 32
+    p.hist_len = p.block_table = p.arrivals = fake
+    p.block_size, p.max_blocks, p.max_hist_len = 16, max_len // 16, max_len
+    fr = _first_round(dev, hkv)
+    S = max_len // 4096 if pieced else 1
+    partials = B * hkv * 4 * S * (128 + 2) * 4
+    sched = (fr + (B - fr) * S) * 16 if pieced else B * 4
+    assert (fr + (B - fr) * (max_len // 4096) <= 65535) == pieced
+    assert _native.attn_workspace_bytes(p) == ((partials + 255) // 256) * 256 + sched
+
+
 @pytest.mark.parametrize("odtype", [torch.bfloat16, torch.float32])
 def test_mfma_decode_pieces_with_recent(dev, odtype):
     """Longest-first pieces on a contiguous ragged batch with an exact recent

@@ -59,6 +59,19 @@ constexpr int kWaitLdsOnly = 0xC07F;
 // s_waitcnt operand that waits for vector memory operations only (vmcnt 0,
 // expcnt and lgkmcnt at their maxima)
 constexpr int kWaitVmemOnly = 0x0F70;
+// Cache policy of the tile loads (buffer-load aux 2 = nt, streaming).  A
+// plain read stream reaches 7.0-7.2 TB/s with nt loads against 6.3-6.45
+// without (MI355X, 1 GiB, every unroll and occupancy tried), and the key rows
+// (1 KB per load instruction, whole lines read once) and the contiguous
+// value rows take it: kernel 179.0-182.2 -> 177.1-180.4 us at c3, 390.4-401.7
+// -> 387.9-400.3 us at c5 (keys; five alternating rounds on three boxes,
+// rocprofv3 averages over ~1,800-3,600 launches each).  The norms, value
+// scales and zeros (runs shorter than a line, lines shared with the
+// neighbouring tile) stay normal: nt there made c3 2-3% slower; so do the
+// paged layout's value loads (32-byte pieces of 512-byte pages: +7.6% at c5).
+constexpr int kKeyPolicy = 2;
+constexpr int kValPolicy = 2;
+constexpr int kSidePolicy = 0;
 
 // Split boundaries.  The grid (KV heads, sequences, splits) is dispatched
 // split-major, so with one round of workgroups, split s of unit u = head +
@@ -223,10 +236,10 @@ struct Pack8 {
     }
   }
   __device__ __forceinline__ void load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kSidePolicy);
     w[0] = a[0]; w[1] = a[1]; w[2] = a[2]; w[3] = a[3];
     if constexpr (sizeof(T) == 4) {
-      const u32x4 c = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16, 0, 0);
+      const u32x4 c = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16, 0, kSidePolicy);
       w[4] = c[0]; w[5] = c[1]; w[6] = c[2]; w[7] = c[3];
     }
   }
@@ -256,9 +269,9 @@ template <typename T>
 struct NormPair {
   uint32_t w[sizeof(T) == 2 ? 1 : 2];
   __device__ __forceinline__ void load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+    w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kSidePolicy);
     // (a second dword load: this toolchain lowers raw_buffer_load_b64 to one dword)
-    if constexpr (sizeof(T) == 4) w[1] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 4, 0);
+    if constexpr (sizeof(T) == 4) w[1] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 4, kSidePolicy);
   }
   __device__ __forceinline__ void load(const T* p) {  // element index even
     if constexpr (sizeof(T) == 2) {
@@ -526,12 +539,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
     } else {
       const auto rv = buf_rsrc(vbytes + d.gA * 32);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) vd[i] = __builtin_amdgcn_raw_buffer_load_b32(rv, offV, 32 * i, 0);
+      for (int i = 0; i < 4; ++i) vd[i] = __builtin_amdgcn_raw_buffer_load_b32(rv, offV, 32 * i, kValPolicy);
     }
   };
   auto fast_keys = [&](const TileDesc& d, u32x4& kqa, u32x4& kqb) {
-    kqa = __builtin_amdgcn_raw_buffer_load_b128(buf_rsrc(kbytes + d.gA * 64), offK, 0, 0);
-    kqb = __builtin_amdgcn_raw_buffer_load_b128(buf_rsrc(kbytes + d.gB * 64), offK, 0, 0);
+    kqa = __builtin_amdgcn_raw_buffer_load_b128(buf_rsrc(kbytes + d.gA * 64), offK, 0, kKeyPolicy);
+    kqb = __builtin_amdgcn_raw_buffer_load_b128(buf_rsrc(kbytes + d.gB * 64), offK, 0, kKeyPolicy);
   };
   // this lane's first softmax token row (tokens tokA, tokA + 1 are consecutive rows)
   auto rowA = [&](const TileDesc& d) -> int64_t { return tokA < 16 ? d.gA + tokA : d.gB + (tokA - 16); };

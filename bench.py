@@ -593,7 +593,7 @@ def cpu_baseline_encode(strat, keys, vals, n: int = 2048):
 
 def copy_ceiling(dev, nbytes: int = 1 << 30, reps: int = 20):
     """The practical HBM ceilings next to the 8 TB/s peak: a plain streaming
-    read of nbytes (smaq_probe_read, 16-byte loads over the whole device; the
+    read of nbytes (smaq_probe_read, 16-byte non-temporal loads; the
     read-bound kernels' ceiling) and a device-to-device copy (read + write
     bytes / time; also the counter-calibration kernel), each the mean of
     `reps` back-to-back launches between HIP events on the launch stream."""

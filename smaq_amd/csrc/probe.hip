@@ -1,13 +1,17 @@
 // Streaming-read probe (smaq_probe_read): the HBM read rate a plain stream of
-// 16-byte loads reaches, the ceiling the bandwidth-bound kernels are judged
-// against next to the published peak.
+// 16-byte non-temporal loads reaches, the ceiling the bandwidth-bound kernels
+// are judged against next to the published peak.  Swept on MI355X (1 GiB;
+// 2, 4, 8 or 16 loads in flight per lane; 1-16 workgroups of 256 threads per
+// CU): nt loads 6.7-7.2 TB/s at 4+ loads in flight, normal loads 5.7-6.5; the
+// fastest shape, below, 7.18.
 #include "attention_internal.h"
 
 namespace smaq {
 
 constexpr int kProbeThreads = 256;
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kProbeUnroll = 4;  // independent 16-byte loads in flight per lane
-constexpr int kProbeBlocksPerCu = 8;
+constexpr int kProbeBlocksPerCu = 2;
 
 __global__ __launch_bounds__(kProbeThreads) void read_probe_kernel(const uint4* __restrict__ src, int64_t n,
                                                                    unsigned int* __restrict__ sink) {
@@ -18,7 +22,8 @@ __global__ __launch_bounds__(kProbeThreads) void read_probe_kernel(const uint4* 
 #pragma unroll
     for (int k = 0; k < kProbeUnroll; ++k) {
       const int64_t j = i + (int64_t)k * kProbeThreads;
-      v[k] = j < n ? src[j] : uint4{0u, 0u, 0u, 0u};
+      const u32x4 x = j < n ? __builtin_nontemporal_load((const u32x4*)(src + j)) : u32x4{0u, 0u, 0u, 0u};
+      v[k] = uint4{x[0], x[1], x[2], x[3]};
     }
 #pragma unroll
     for (int k = 0; k < kProbeUnroll; ++k) {

@@ -65,10 +65,12 @@ constexpr int kWaitVmemOnly = 0x0F70;
 // (1 KB per load instruction, whole lines read once) and the contiguous
 // value rows take it: kernel 179.0-182.2 -> 177.1-180.4 us at c3, 390.4-401.7
 // -> 387.9-400.3 us at c5 (keys; five alternating rounds on three boxes,
-// rocprofv3 averages over ~1,800-3,600 launches each).  The norms, value
-// scales and zeros (runs shorter than a line, lines shared with the
-// neighbouring tile) stay normal: nt there made c3 2-3% slower; so do the
-// paged layout's value loads (32-byte pieces of 512-byte pages: +7.6% at c5).
+// rocprofv3 averages over ~1,800-3,600 launches each).  The norms (64-byte
+// runs, their lines shared with the neighbouring tile) and the value scales
+// and zeros (two whole lines per tile, each 16 bytes read by four lanes)
+// stay normal: nt on all three made c3 2-3% slower, on the scales and zeros
+// alone 3.6%; so do the paged layout's value loads (32-byte pieces of
+// 512-byte pages: +7.6% at c5).
 constexpr int kKeyPolicy = 2;
 constexpr int kValPolicy = 2;
 constexpr int kSidePolicy = 0;

@@ -302,6 +302,13 @@ typedef struct smaq_attn_params {
   int q_raw_dtype;
   const float* rot_mt;
   const float* rot_scale;
+  /* Rows in each history pool array (key codes, norms, values, scales,
+     zeros share the row index; paged layout: blocks * n_kv_heads *
+     block_size), or 0 if unknown.  Lets the decode kernel address a paged
+     value pool below 4 GB through one buffer descriptor (range-checked:
+     rows past it read as zero); 0 keeps 64-bit per-lane addresses.  Added
+     last, so a zero-initialised struct keeps its earlier meaning. */
+  long long hist_rows;
 } smaq_attn_params;
 
 /* Bytes of workspace smaq_attn_hybrid needs for these parameters. */

@@ -54,6 +54,7 @@ class AttnParams(ctypes.Structure):
         ("phases", c_int), ("impl", c_int),
         ("arrivals", c_void_p),
         ("q_raw", c_void_p), ("q_raw_dtype", c_int), ("rot_mt", c_void_p), ("rot_scale", c_void_p),
+        ("hist_rows", c_ll),
     ]
 
 

@@ -728,6 +728,7 @@ extern "C" int smaq_attn_hybrid(const smaq_attn_params* pp, void* stream) {
   } else if (pl.s_hist > 0 && (phases & 1)) {
     HistAddr a{p.hist_seq_start, p.max_hist_len, p.hist_head_stride, p.block_table, p.max_blocks,
                p.block_size, p.n_kv_heads};
+    a.rows = p.hist_rows > 0 ? p.hist_rows : 0;
     int rc = SMAQ_EUNSUPPORTED;
     if (pl.mfma) {
       int* order = (int*)sched;

@@ -22,6 +22,7 @@ struct HistAddr {
   long long head_stride;
   const int* table;
   int max_blocks, block_size, n_kv;
+  long long rows = 0;  // rows in each pool array, 0 if unknown
   __device__ __forceinline__ int64_t row(int b, int h, int64_t t) const {
     if (table) {
       const int blk = table[(int64_t)b * max_blocks + t / block_size];

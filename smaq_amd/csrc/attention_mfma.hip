@@ -200,6 +200,10 @@ __device__ __forceinline__ float dpp_row_ror(float x) {
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, -1, 0x00020000);
 }
+// a descriptor over `bytes` bytes from base (loads past them read zero)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc_n(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
 
 // (x & m) | c.  Plain code, not inline asm, so that the compiler sees the VALU
 // write and keeps the wait states the matrix core needs before reading the
@@ -352,7 +356,12 @@ __device__ __forceinline__ f32x2 load_agent2(const float* a) {
   return __builtin_bit_cast(f32x2, __hip_atomic_load((const uint64_t*)a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
 }
 
-template <int KBITS, typename TN, typename TV, bool SPLIT>
+// VBUF (16-token pages, a value pool below 4 GB): the value loads address the
+// pool through one descriptor with 32-bit lane offsets instead of 64-bit
+// per-lane addresses (c5 kernel 398.6-399.1 -> 394.7-395.5 us and
+// 378.5-378.9 -> 374.2-374.8 us, three alternating rounds on each of two
+// boxes; non-temporal there was slower: 421.5-425.3 us)
+template <int KBITS, typename TN, typename TV, bool SPLIT, bool VBUF>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWaves<TN, TV>, kDecodeWaves<TN, TV>))) void decode_mfma_kernel(
     smaq_attn_params p, HistAddr addr, Partials part, SplitRule rule, const int* __restrict__ order) {
   // key LUT, one 8-byte entry per code byte: {f16 hi pair, f16 lo pair}
@@ -482,6 +491,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
   s1 = uniform64(s1);
   const uint8_t* kbytes = (const uint8_t*)p.key_bytes;
   const uint8_t* vbytes = (const uint8_t*)p.val_bytes;
+  // (VBUF: the value pool, 32-byte rows, as one range-checked descriptor)
+  const auto vpool = buf_rsrc_n(vbytes, VBUF ? (uint32_t)addr.rows * 32u : 0u);
   const TN* norms = (const TN*)p.key_norms;
   const TV* vsc = (const TV*)p.val_scales;
   const TV* vzr = (const TV*)p.val_zeros;
@@ -534,7 +545,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWave
   const uint32_t offK = (uint32_t)(n * 64 + 16 * kg);
   const uint32_t offV = (uint32_t)(128 * tq + 4 * pq);  // rows 4tq.. (both groups when gB = gA + 16)
   auto fast_values = [&](const TileDesc& d, uint32_t* vd) {
-    if constexpr (SPLIT) {
+    if constexpr (SPLIT && VBUF) {
+      // (the rows fit 32 bits: the pool is below 4 GB)
+      const uint32_t vo = ((uint32_t)(tq < 4 ? d.gA : d.gB) + 4u * (uint32_t)(tq & 3)) * 32u + 4u * (uint32_t)pq;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vd[i] = __builtin_amdgcn_raw_buffer_load_b32(vpool, vo, 32 * i, 0);
+    } else if constexpr (SPLIT) {
       const uint8_t* vrow = vbytes + ((tq < 4 ? d.gA : d.gB) + 4 * (tq & 3)) * 32 + 4 * pq;
 #pragma unroll
       for (int i = 0; i < 4; ++i) vd[i] = *(const uint32_t*)(vrow + 32 * i);
@@ -1188,7 +1204,7 @@ int64_t mfma_decode_split_len(const smaq_attn_params& p) {
 constexpr int kSplitTilt4 = 10;
 static_assert(kSplitTilt4 * 3 < kSplitWeight, "split weights must stay positive");
 
-template <int KB, typename TN, bool SPLIT>
+template <int KB, typename TN, bool SPLIT, bool VBUF>
 static void launch_v(const smaq_attn_params& p, const HistAddr& a, const Partials& part, const SplitRule& rule,
                      int n_splits, const int* order, hipStream_t st) {
   // heads fastest, then sequences (the longest-first order when given), then
@@ -1196,9 +1212,9 @@ static void launch_v(const smaq_attn_params& p, const HistAddr& a, const Partial
   // in item mode, heads fastest, then items
   const dim3 grid(p.n_kv_heads, rule.pieces ? rule.items : p.batch, rule.pieces ? 1 : n_splits);
   switch (p.val_dtype) {
-    case SMAQ_F32: hipLaunchKernelGGL((decode_mfma_kernel<KB, TN, float, SPLIT>), grid, dim3(256), 0, st, p, a, part, rule, order); break;
-    case SMAQ_F16: hipLaunchKernelGGL((decode_mfma_kernel<KB, TN, _Float16, SPLIT>), grid, dim3(256), 0, st, p, a, part, rule, order); break;
-    default: hipLaunchKernelGGL((decode_mfma_kernel<KB, TN, bf16, SPLIT>), grid, dim3(256), 0, st, p, a, part, rule, order); break;
+    case SMAQ_F32: hipLaunchKernelGGL((decode_mfma_kernel<KB, TN, float, SPLIT, VBUF>), grid, dim3(256), 0, st, p, a, part, rule, order); break;
+    case SMAQ_F16: hipLaunchKernelGGL((decode_mfma_kernel<KB, TN, _Float16, SPLIT, VBUF>), grid, dim3(256), 0, st, p, a, part, rule, order); break;
+    default: hipLaunchKernelGGL((decode_mfma_kernel<KB, TN, bf16, SPLIT, VBUF>), grid, dim3(256), 0, st, p, a, part, rule, order); break;
   }
 }
 
@@ -1206,8 +1222,14 @@ template <int KB, typename TN>
 static void launch_s(const smaq_attn_params& p, const HistAddr& a, const Partials& part, const SplitRule& rule,
                      int n_splits, const int* order, hipStream_t st) {
   // 16-token pages put a tile's two 16-token groups in different blocks
-  if (p.block_table && p.block_size == 16) launch_v<KB, TN, true>(p, a, part, rule, n_splits, order, st);
-  else launch_v<KB, TN, false>(p, a, part, rule, n_splits, order, st);
+  // (value rows of 32 bytes: the pool's bytes as a 32-bit descriptor range)
+  const bool vbuf = a.rows > 0 && a.rows <= (int64_t)(0xFFFFFFFFu / 32u);
+  if (p.block_table && p.block_size == 16) {
+    if (vbuf) launch_v<KB, TN, true, true>(p, a, part, rule, n_splits, order, st);
+    else launch_v<KB, TN, true, false>(p, a, part, rule, n_splits, order, st);
+  } else {
+    launch_v<KB, TN, false, false>(p, a, part, rule, n_splits, order, st);
+  }
 }
 
 template <int KB>

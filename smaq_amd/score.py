@@ -153,6 +153,9 @@ class AttentionPlan:
                 p.vq_blocks, p.vq_block_dim, p.vq_centroids = fused.n_blocks, fused.block_dim, fused.n_centroids
             p.val_bytes = val_data.data_ptr()
             p.val_row_bytes = val_data.shape[-1]
+            # rows the pools hold (the decode kernel's range-checked value
+            # addressing); 0 when the value array is not one dense block
+            p.hist_rows = val_data.numel() // max(1, val_data.shape[-1]) if val_data.is_contiguous() else 0
             p.val_bits, p.val_group = val_bits, val_group
             p.val_scales, p.val_zeros = val_scales.data_ptr(), val_zeros.data_ptr()
             p.val_dtype = _native.dtype_code(val_scales.dtype)

@@ -555,3 +555,34 @@ def test_nan_key_norm_gives_nan_rows(dev, lens):
     out = kvb.attention(q16, impl=3).cpu()
     assert bool(torch.isnan(out[0, :, g:2 * g]).all()), "prefill"
     assert not bool(torch.isnan(out[0, :, :g]).any()) and not bool(torch.isnan(out[1:]).any()), "prefill"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_mfma_decode_paged_value_descriptor_bits(dev, dtype):
+    """16-token pages: the plan records the pools' row count (hist_rows), and
+    the decode kernel then reads the value pool through one range-checked
+    descriptor with 32-bit lane offsets.  Same bits as the 64-bit per-lane
+    addresses it takes with hist_rows = 0 (ragged lengths, one sequence of
+    5,000 tokens), and the oracle's result for a sample."""
+    strat, codec = _codec_pair(dev, 3, 420)
+    gen = torch.Generator().manual_seed(421)
+    hkv, bs = 8, 16
+    B = 40
+    lens = [int(x) for x in torch.randint(1, 900, (B,), generator=gen)]
+    lens[3] = 5000
+    table, nphys = _paged_table(lens, bs, gen)
+    keys = [sample_keys(n * hkv, seed=430 + b).reshape(n, hkv, 128).to(dtype) for b, n in enumerate(lens)]
+    vals = [torch.randn(n, hkv, 128, generator=gen).to(dtype) for n in lens]
+    pk = PagedQuantizedKV.encode(strat, [k.to(dev) for k in keys], [v.to(dev) for v in vals], table.to(dev),
+                                 num_blocks=nphys, block_size=bs)
+    q = torch.randn(B, 32, 128, generator=gen).to(dtype)
+    plan = pk.plan(q.to(dev), impl=2)
+    assert plan.params.hist_rows == nphys * hkv * bs
+    desc = plan.run(q.to(dev)).clone()
+    plan.params.hist_rows = 0
+    addr = plan.run(q.to(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(desc, addr), "value descriptor and per-lane addresses differ"
+    for b in (0, 3, B - 1):
+        assert_attn_close(desc[b:b + 1].squeeze(1), _oracle(codec, keys[b], vals[b], q[b:b + 1], 32, hkv),
+                          f"paged value descriptor {dtype} seq {b}")

@@ -360,7 +360,9 @@ __device__ __forceinline__ f32x2 load_agent2(const float* a) {
 // pool through one descriptor with 32-bit lane offsets instead of 64-bit
 // per-lane addresses (c5 kernel 398.6-399.1 -> 394.7-395.5 us and
 // 378.5-378.9 -> 374.2-374.8 us, three alternating rounds on each of two
-// boxes; non-temporal there was slower: 421.5-425.3 us)
+// boxes; non-temporal there was slower: 421.5-425.3 us; so were the norms,
+// scales and zeros through such descriptors as well: 373.6-373.9 against
+// 371.6-371.9 us)
 template <int KBITS, typename TN, typename TV, bool SPLIT, bool VBUF>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kDecodeWaves<TN, TV>, kDecodeWaves<TN, TV>))) void decode_mfma_kernel(
     smaq_attn_params p, HistAddr addr, Partials part, SplitRule rule, const int* __restrict__ order) {

@@ -305,9 +305,10 @@ typedef struct smaq_attn_params {
   /* Rows in each history pool array (key codes, norms, values, scales,
      zeros share the row index; paged layout: blocks * n_kv_heads *
      block_size), or 0 if unknown.  Lets the decode kernel address a paged
-     value pool below 4 GB through one buffer descriptor (range-checked:
-     rows past it read as zero); 0 keeps 64-bit per-lane addresses.  Added
-     last, so a zero-initialised struct keeps its earlier meaning. */
+     value pool below 4 GB through one buffer descriptor; it must cover
+     every row the block table reaches (the descriptor is range-checked:
+     value rows past it read as zero).  0 keeps 64-bit per-lane addresses.
+     Added last, so a zero-initialised struct keeps its earlier meaning. */
   long long hist_rows;
 } smaq_attn_params;
 

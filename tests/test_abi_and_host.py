@@ -233,3 +233,32 @@ def test_fake_layer_namespace_idiom():
     assert not info.unified_kv
     fake = types.SimpleNamespace(shape=(1, 8, 16, 128))
     assert fake.shape[-1] == 128
+
+
+def test_attn_params_mirror_the_header():
+    """The ctypes AttnParams lists the fields of include/smaq_hip.h's
+    smaq_attn_params in the same order with the same kinds (int, float,
+    long long, pointer), hist_rows last: the struct layout both sides read."""
+    import re
+    from pathlib import Path
+    hdr = (Path(__file__).resolve().parents[1] / "include" / "smaq_hip.h").read_text()
+    body = hdr[hdr.index("typedef struct smaq_attn_params {"):hdr.index("} smaq_attn_params;")]
+    body = re.sub(r"/\*.*?\*/", "", body.split("{", 1)[1], flags=re.S)
+    fields = []
+    for decl in body.split(";"):
+        decl = " ".join(decl.split())
+        if not decl:
+            continue
+        m = re.match(r"((?:const )?(?:unsigned )?(?:long long|int|float|void|char)\s*\**)\s*(.*)", decl)
+        assert m, decl
+        base, names = m.group(1), m.group(2)
+        for nm in names.split(","):
+            nm = nm.strip()
+            ptr = "*" in base or nm.startswith("*")
+            nm = nm.lstrip("*").strip()
+            kind = "ptr" if ptr else ("ll" if "long long" in base else ("float" if "float" in base else "int"))
+            fields.append((nm, kind))
+    kinds = {ctypes.c_int: "int", ctypes.c_float: "float", ctypes.c_longlong: "ll", ctypes.c_void_p: "ptr"}
+    mirror = [(nm, kinds[t]) for nm, t in _native.AttnParams._fields_]
+    assert mirror == fields
+    assert fields[-1] == ("hist_rows", "ll")

@@ -580,9 +580,13 @@ def test_mfma_decode_paged_value_descriptor_bits(dev, dtype):
     assert plan.params.hist_rows == nphys * hkv * bs
     desc = plan.run(q.to(dev)).clone()
     plan.params.hist_rows = 0
-    addr = plan.run(q.to(dev))
+    addr = plan.run(q.to(dev)).clone()
+    # a row count past the 4 GB limit: the per-lane addresses again
+    plan.params.hist_rows = 1 << 28
+    big = plan.run(q.to(dev))
     torch.cuda.synchronize()
     assert torch.equal(desc, addr), "value descriptor and per-lane addresses differ"
+    assert torch.equal(big, addr), "a pool above 4 GB must take the per-lane addresses"
     for b in (0, 3, B - 1):
         assert_attn_close(desc[b:b + 1].squeeze(1), _oracle(codec, keys[b], vals[b], q[b:b + 1], 32, hkv),
                           f"paged value descriptor {dtype} seq {b}")

@@ -69,8 +69,8 @@ constexpr int kWaitVmemOnly = 0x0F70;
 // runs, their lines shared with the neighbouring tile) and the value scales
 // and zeros (two whole lines per tile, each 16 bytes read by four lanes)
 // stay normal: nt on all three made c3 2-3% slower, on the scales and zeros
-// alone 3.6%; so do the paged layout's value loads (32-byte pieces of
-// 512-byte pages: +7.6% at c5).
+// alone 3.6%, on the norms alone 1.1%; so do the paged layout's value loads
+// (32-byte pieces of 512-byte pages: +7.6% at c5).
 constexpr int kKeyPolicy = 2;
 constexpr int kValPolicy = 2;
 constexpr int kSidePolicy = 0;
